@@ -1,0 +1,305 @@
+"""Benchmark of the KV-cache attention path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+
+A step is one decode-attention op of config 2 (Llama-3-8B shape: 32 query
+heads on 8 KV heads, hd 128, 4096 cached rows): append the step's K, V row
+(kv_append) and attend 4097 rows (split-KV decode kernel), through the C ABI.
+Steps rotate over `layers` distinct KV states (>= 512 MiB together, as a
+real model's 32 layers are), so K and V come from HBM, not the 256 MB
+Infinity Cache. Inputs are resident in HBM before the timed region.
+
+One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time),
+roofline of the decode kernel (HIP-event kernel time), the CPU oracle timed on
+this host, and the other configs' figures (prefill TFLOP/s, ragged decode,
+ViT) under "extra".
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from synapse_amd import capi  # noqa: E402
+from synapse_amd import workloads as wl  # noqa: E402
+from synapse_amd.capi import SYN_F16, SYN_F32, Arena, AttnDesc, SelfDesc, SeqDesc, check, lib  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 matrix, TFLOP/s
+
+
+class Hip:
+    """HIP events on the arena's stream, via the HIP runtime the library uses."""
+
+    def __init__(self):
+        self.rt = ctypes.CDLL("libamdhip64.so")
+        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def events(self, n: int) -> list:
+        out = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            assert self.rt.hipEventCreate(ctypes.byref(e)) == 0
+            out.append(e)
+        return out
+
+    def record(self, ev, stream) -> None:
+        assert self.rt.hipEventRecord(ev, stream) == 0
+
+    def ms(self, a, b) -> float:
+        assert self.rt.hipEventSynchronize(b) == 0
+        t = ctypes.c_float()
+        assert self.rt.hipEventElapsedTime(ctypes.byref(t), a, b) == 0
+        return float(t.value)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int):
+    """Config 2: returns (ms_per_step, kernel_ms_avg, details)."""
+    row = cfg.n_kv * cfg.head_dim
+    max_ctx = cfg.ctx + 1
+    state = capi.kv_state_bytes(max_ctx, cfg.n_kv, cfg.head_dim)
+    qsz = cfg.n_heads * cfg.head_dim
+    scratch_bytes = int(lib().syn_hip_attention_scratch_bytes(cfg.n_heads, cfg.n_kv, cfg.head_dim, max_ctx, 1))
+    per_layer = state + capi.align(qsz * 4) * 2 + capi.align(row * 4) * 2 + 4096
+    arena = Arena(layers * per_layer + scratch_bytes + (1 << 20))
+    kc, vc, q, k, v = wl.decode_inputs(cfg)
+    scratch = arena.alloc(scratch_bytes)
+    descs = []
+    for _ in range(layers):
+        cache = capi.kv_state(arena, max_ctx, cfg.n_kv, cfg.head_dim)
+        capi.upload_cache(arena, cache, kc, vc)
+        d = AttnDesc(cache=cache, q_offset=arena.put(q), k_offset=arena.put(k), v_offset=arena.put(v),
+                     out_offset=arena.alloc(qsz * 4), scratch_offset=scratch, scratch_bytes=scratch_bytes,
+                     n_heads=cfg.n_heads, pos=cfg.ctx, n=1, scale=cfg.scale, q_dtype=SYN_F32, kv_dtype=SYN_F32)
+        descs.append(d)
+    arena.sync()
+    stream = arena.stream
+    L = lib()
+    for i in range(warmup):
+        check(L.syn_hip_attention(arena.handle, ctypes.byref(descs[i % layers])))
+    arena.sync()
+    # Timed region 1: whole steps (append + attend), back to back.
+    t0, t1 = hip.events(2)
+    hip.record(t0, stream)
+    w0 = time.perf_counter()
+    for i in range(steps):
+        check(L.syn_hip_attention(arena.handle, ctypes.byref(descs[i % layers])))
+    hip.record(t1, stream)
+    step_ms = hip.ms(t0, t1) / steps
+    wall_ms = (time.perf_counter() - w0) * 1e3 / steps
+    # Timed region 2: the decode kernel alone, bracketed by events per launch.
+    evs = hip.events(2 * steps)
+    for i in range(steps):
+        d = descs[i % layers]
+        hip.record(evs[2 * i], stream)
+        check(L.syn_hip_attend(arena.handle, ctypes.byref(d)))
+        hip.record(evs[2 * i + 1], stream)
+    kern = [hip.ms(evs[2 * i], evs[2 * i + 1]) for i in range(steps)]
+    out = arena.download(descs[0].out_offset, (qsz,), np.float32)
+    assert np.all(np.isfinite(out))
+    arena.close()
+    return step_ms, float(np.mean(kern)), {"wall_ms_per_step": wall_ms, "kernel_ms_median": float(np.median(kern))}
+
+
+def bench_prefill(hip: Hip, cfg: wl.Prefill, reps: int):
+    """Config 3: the flash kernel alone (cache already appended) and the
+    whole op (append + attend)."""
+    qsz = cfg.n_heads * cfg.head_dim
+    row = cfg.n_kv * cfg.head_dim
+    arena = Arena(capi.kv_state_bytes(cfg.n, cfg.n_kv, cfg.head_dim) + cfg.n * (qsz * 6 + row * 4) + (8 << 20))
+    q, k, v = wl.prefill_inputs(cfg)
+    cache = capi.kv_state(arena, cfg.n, cfg.n_kv, cfg.head_dim)
+    d = AttnDesc(cache=cache, q_offset=arena.put(q.astype(np.float16)), k_offset=arena.put(k.astype(np.float16)),
+                 v_offset=arena.put(v.astype(np.float16)), out_offset=arena.alloc(cfg.n * qsz * 4),
+                 scratch_offset=0, scratch_bytes=0, n_heads=cfg.n_heads, pos=0, n=cfg.n, scale=cfg.scale,
+                 q_dtype=SYN_F16, kv_dtype=SYN_F16)
+    L = lib()
+    check(L.syn_hip_attention(arena.handle, ctypes.byref(d)))
+    arena.sync()
+    stream = arena.stream
+    evs = hip.events(2 * reps)
+    for i in range(reps):
+        hip.record(evs[2 * i], stream)
+        check(L.syn_hip_attend(arena.handle, ctypes.byref(d)))
+        hip.record(evs[2 * i + 1], stream)
+    kern = [hip.ms(evs[2 * i], evs[2 * i + 1]) for i in range(reps)]
+    t0, t1 = hip.events(2)
+    hip.record(t0, stream)
+    for i in range(reps):
+        check(L.syn_hip_attention(arena.handle, ctypes.byref(d)))
+    hip.record(t1, stream)
+    op_ms = hip.ms(t0, t1) / reps
+    arena.close()
+    return float(np.mean(kern)), op_ms
+
+
+def bench_ragged(hip: Hip, cfg: wl.Ragged, reps: int):
+    lengths = [int(x) for x in cfg.lengths()]
+    row = cfg.n_kv * cfg.head_dim
+    qsz = cfg.n_heads * cfg.head_dim
+    total = sum(capi.kv_state_bytes(L, cfg.n_kv, cfg.head_dim) for L in lengths)
+    arena = Arena(total + cfg.n_seqs * qsz * 8 + (64 << 20))
+    g = wl.rng(wl.SEED + 9)
+    seqs = []
+    for L in lengths:
+        cache = capi.kv_state(arena, L, cfg.n_kv, cfg.head_dim)
+        kc = wl.to_f16_bits(wl.normal(g, (L, row)))
+        capi.upload_cache(arena, cache, kc, kc)
+        seqs.append(SeqDesc(cache=cache, q_offset=arena.put(wl.normal(g, (qsz,))), out_offset=arena.alloc(qsz * 4),
+                            pos=L - 1))
+    arr = (SeqDesc * len(seqs))(*seqs)
+    need = int(lib().syn_hip_attend_batch_scratch_bytes(arr, len(seqs), cfg.n_heads))
+    scratch = arena.alloc(need)
+    L_ = lib()
+    call = lambda: check(L_.syn_hip_attend_batch(arena.handle, arr, len(seqs), cfg.n_heads, cfg.scale, SYN_F32,
+                                                 scratch, need))
+    call()
+    arena.sync()
+    t0, t1 = hip.events(2)
+    hip.record(t0, arena.stream)
+    for _ in range(reps):
+        call()
+    hip.record(t1, arena.stream)
+    ms = hip.ms(t0, t1) / reps
+    nbytes = sum(L * row * 2 * 2 for L in lengths) + cfg.n_seqs * qsz * 8
+    arena.close()
+    return ms, nbytes
+
+
+def bench_vision(hip: Hip, cfg: wl.Vision, reps: int):
+    rows = cfg.batch * cfg.n
+    size = cfg.n_heads * cfg.head_dim
+    arena = Arena(rows * size * (3 * 2 + 4) + (8 << 20))
+    q, k, v = wl.vision_inputs(cfg)
+    d = SelfDesc(q_offset=arena.put(q.astype(np.float16)), k_offset=arena.put(k.astype(np.float16)),
+                 v_offset=arena.put(v.astype(np.float16)), out_offset=arena.alloc(rows * size * 4), n=cfg.n,
+                 batch=cfg.batch, n_heads=cfg.n_heads, head_dim=cfg.head_dim, scale=cfg.scale, in_dtype=SYN_F16)
+    L = lib()
+    check(L.syn_hip_self_attention(arena.handle, ctypes.byref(d)))
+    arena.sync()
+    t0, t1 = hip.events(2)
+    hip.record(t0, arena.stream)
+    for _ in range(reps):
+        check(L.syn_hip_self_attention(arena.handle, ctypes.byref(d)))
+    hip.record(t1, arena.stream)
+    ms = hip.ms(t0, t1) / reps
+    arena.close()
+    return ms
+
+
+def cpu_baseline(cfg: wl.Decode, budget_s: float):
+    """The CPU oracle (oracle/liboracle.so, a port of the reference's
+    attention()) timed on this host: full config-2 decode steps, threads over
+    the 8 KV groups as the reference's session splits them."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import binding as orc
+
+    kc, vc, q, k, v = wl.decode_inputs(cfg)
+    ok_k, ok_v = orc.new_cache(cfg.ctx + 1, cfg.n_kv, cfg.head_dim)
+    ok_k[: cfg.ctx], ok_v[: cfg.ctx] = kc, vc
+    threads = min(cfg.n_kv, len(os.sched_getaffinity(0)))
+    scores = np.zeros(orc.scratch_floats(cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.ctx + 1), np.float32)
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < 3:
+        t = time.perf_counter()
+        orc.attend_rows(q, cfg.ctx, ok_k, ok_v, cfg.n_heads, cfg.scale, threads=threads, scores=scores)
+        times.append(time.perf_counter() - t)
+    best = min(times)
+    return {"value": round(cfg.kv_bytes() / best / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} config-2 decode steps (attend over 4097 cached rows, 32 heads), best of "
+                      f"{len(times)}; oracle/liboracle.so, {threads} threads over KV groups, "
+                      f"{os.cpu_count()} host CPUs visible",
+            "ms_per_step": round(best * 1e3, 3)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--layers", type=int, default=40, help="distinct KV states rotated over (>= 32)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-only", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the attention path is built and measured on a single MI355X "
+              "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+        return 2
+
+    hip = Hip()
+    cfg = wl.C2
+    log(f"decode {cfg.name}: {args.steps} steps, {args.warmup} warmup, {args.layers} rotating KV states")
+    step_ms, kern_ms, det = bench_decode(hip, cfg, args.steps, args.warmup, args.layers)
+    nbytes = cfg.kv_bytes()
+    value = nbytes / (step_ms * 1e-3) / 1e9
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    log(f"decode: {step_ms * 1e3:.2f} us/step, kernel {kern_ms * 1e3:.2f} us -> {achieved:.0f} GB/s")
+    extra = {"decode_kernel_us": round(kern_ms * 1e3, 3), "decode_step_us": round(step_ms * 1e3, 3),
+             "decode_tokens_per_s_32_layers": round(1e3 / (step_ms * 32), 1),
+             "decode_wall_us_per_step": round(det["wall_ms_per_step"] * 1e3, 3),
+             "decode_kernel_us_median": round(det["kernel_ms_median"] * 1e3, 3)}
+
+    if not args.decode_only:
+        p = wl.C3
+        log(f"prefill {p.name}")
+        kms, op_ms = bench_prefill(hip, p, 50)
+        tf = p.flops() / (kms * 1e-3) / 1e12
+        extra["prefill"] = {"kernel_us": round(kms * 1e3, 2), "tflops": round(tf, 1),
+                            "frac_of_f16_peak": round(tf / MFMA_F16_PEAK_TFS, 4),
+                            "op_us_with_append": round(op_ms * 1e3, 2),
+                            "tokens_per_s": round(p.n / (op_ms * 1e-3), 0), "flops": p.flops()}
+        log(f"prefill: {kms * 1e3:.1f} us, {tf:.0f} TFLOP/s")
+        r = wl.C4
+        log(f"ragged {r.name}")
+        rms, rbytes = bench_ragged(hip, r, 20)
+        extra["ragged"] = {"us": round(rms * 1e3, 2), "gbs": round(rbytes / (rms * 1e-3) / 1e9, 1),
+                           "frac_of_hbm": round(rbytes / (rms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": rbytes,
+                           "seqs_per_s": round(r.n_seqs / (rms * 1e-3), 0)}
+        vcfg = wl.C5
+        log(f"vision {vcfg.name}")
+        vms = bench_vision(hip, vcfg, 50)
+        extra["vision"] = {"us": round(vms * 1e3, 2), "tflops": round(vcfg.flops() / (vms * 1e-3) / 1e12, 1),
+                           "gbs": round(vcfg.bytes() / (vms * 1e-3) / 1e9, 1),
+                           "images_per_s": round(vcfg.batch / (vms * 1e-3), 0)}
+
+    line = {
+        "metric": "decode attn HBM GB/s (8B GQA, KV 4k) + prefill attn TFLOP/s; % roofline",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (seeded PCG64; K RoPE'd, theta 500000)",
+        "config": {"workload": "config 2: Llama-3-8B decode attention, H=32, Hkv=8, hd=128, 4096 cached rows "
+                               "+ 1 appended (append + attend per step)",
+                   "kv_states_rotated": args.layers, "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+        "extra": extra,
+    }
+    if not args.no_cpu:
+        log("cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,203 @@
+/* synapse_hip.h — C ABI of the MI355X (gfx950) KV-cache attention library.
+ *
+ * The drop-in boundary for synapse's attention path (branes-ai/synapse
+ * v0.15.12; S/ = sdk/include/branes/synapse/). A host session calls these
+ * from its two attention executor hooks, session::execute(op_attention)
+ * (S/graph/session.hpp:348-374) and session::execute(op_self_attention)
+ * (S/graph/session.hpp:409-449). Plain pointers, sizes and POD descriptors
+ * only; no C++ or framework types cross this interface, and no exception
+ * does: every call returns SYN_HIP_OK (0) or an error code.
+ *
+ * Memory model. The library owns one device arena per session (one
+ * hipMalloc at creation). Every tensor, scratch buffer and KV state a call
+ * touches is named by its byte offset into that arena, so the library can
+ * bounds-check every descriptor on the host before it launches anything.
+ * All work of one arena runs in order on the arena's own HIP stream.
+ *
+ * KV state layout (one layer, all halves = IEEE binary16):
+ *   K   at k_offset: [max_ctx][n_kv_heads][head_dim]   row-major, as the
+ *       reference stores K (S/kernels/attention.hpp:131-143);
+ *   V^T at v_offset: [n_kv_heads][head_dim][ctx_stride] — V is stored
+ *       TRANSPOSED (position fastest), ctx_stride = syn_hip_kv_ctx_stride().
+ *       The reference keeps V row-major; the transposed layout lets the
+ *       P.V matrix-core step read its operand straight from memory.
+ * Row tensors are [n][size] floats (or halves where a dtype says so).
+ */
+#ifndef SYNAPSE_HIP_H
+#define SYNAPSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum {
+    SYN_HIP_OK = 0,
+    SYN_HIP_EINVAL = -1,       /* bad argument or descriptor (shape, scale, dtype) */
+    SYN_HIP_ERANGE = -2,       /* an offset + extent falls outside the arena */
+    SYN_HIP_EUNSUPPORTED = -3, /* a shape this build has no kernel for */
+    SYN_HIP_ENOMEM = -4,       /* device allocation failed */
+    SYN_HIP_ENODEV = -5        /* no gfx950 device, or the HIP runtime failed to start */
+    /* positive values: a hipError_t returned by the HIP runtime */
+};
+
+/* Element types of row tensors. */
+enum { SYN_F32 = 0, SYN_F16 = 1 };
+
+typedef struct syn_arena syn_arena;
+
+/* Text for a status code; never NULL. */
+const char* syn_hip_error_string(int status);
+/* The last error's detail on this thread ("" if none). */
+const char* syn_hip_last_error(void);
+
+/* ---- arena (session construction / destruction) ------------------------
+ * Replaces session's arena + states allocation (S/graph/session.hpp:90-95,
+ * :193-197) with one device allocation of `bytes` bytes, 256-B aligned, on
+ * the current HIP device, plus the library's own control words (zeroed). */
+int syn_hip_arena_create(size_t bytes, syn_arena** out);
+int syn_hip_arena_destroy(syn_arena* arena);
+size_t syn_hip_arena_bytes(const syn_arena* arena);
+/* The arena's hipStream_t, for callers that record events on it. */
+void* syn_hip_arena_stream(syn_arena* arena);
+
+/* Host <-> arena copies, in stream order; download waits for completion.
+ * Stand-ins for reading and writing session::tensor() (S/graph/session.hpp:107-110). */
+int syn_hip_upload(syn_arena* arena, uint64_t offset, const void* host, size_t bytes);
+int syn_hip_download(syn_arena* arena, uint64_t offset, void* host, size_t bytes);
+/* Byte fill, as session::reset() zeroes the states (S/graph/session.hpp:127-129). */
+int syn_hip_fill(syn_arena* arena, uint64_t offset, int value, size_t bytes);
+/* Copy within the arena. */
+int syn_hip_copy(syn_arena* arena, uint64_t dst, uint64_t src, size_t bytes);
+/* Wait for all work queued on the arena. */
+int syn_hip_synchronize(syn_arena* arena);
+
+/* ---- KV state sizing ----------------------------------------------------
+ * V^T row length in halves for a cache of max_ctx positions (padded so every
+ * row starts 128-B aligned). */
+uint32_t syn_hip_kv_ctx_stride(uint32_t max_ctx);
+/* Device bytes of one KV state: K block (256-B aligned) then V^T block. The
+ * reference's state_desc::bytes (2*2*max_ctx*n_kv*hd, S/graph/graph.hpp:707-716)
+ * is the unpadded size of the same data. */
+uint64_t syn_hip_kv_state_bytes(uint32_t max_ctx, uint32_t n_kv_heads, uint32_t head_dim);
+
+typedef struct syn_kv_desc {
+    uint64_t k_offset;   /* K block */
+    uint64_t v_offset;   /* V^T block */
+    uint32_t max_ctx;
+    uint32_t n_kv_heads;
+    uint32_t head_dim;   /* even, <= 256 (S/kernels/attention.hpp:44) */
+    uint32_t ctx_stride; /* = syn_hip_kv_ctx_stride(max_ctx) */
+} syn_kv_desc;
+
+/* ---- causal attention over a KV cache ----------------------------------- */
+typedef struct syn_attn_desc {
+    syn_kv_desc cache;
+    uint64_t q_offset;       /* n rows of n_heads*head_dim, type q_dtype */
+    uint64_t k_offset;       /* n rows of n_kv_heads*head_dim, type kv_dtype: the run's new K */
+    uint64_t v_offset;       /* n rows of n_kv_heads*head_dim, type kv_dtype: the run's new V */
+    uint64_t out_offset;     /* n rows of n_heads*head_dim f32 */
+    uint64_t scratch_offset; /* split-KV partials; see syn_hip_attention_scratch_bytes */
+    uint64_t scratch_bytes;
+    uint32_t n_heads;        /* a multiple of cache.n_kv_heads */
+    uint32_t pos;            /* position of the run's first token */
+    uint32_t n;              /* tokens in the run, >= 1; pos + n <= cache.max_ctx */
+    float scale;             /* finite, > 0 */
+    uint32_t q_dtype;        /* SYN_F32 or SYN_F16 */
+    uint32_t kv_dtype;       /* SYN_F32 or SYN_F16 */
+} syn_attn_desc;
+
+/* Scratch bytes syn_hip_attention needs for runs of up to max_batch tokens
+ * against a cache of max_ctx positions. The GPU counterpart of
+ * attention_scratch_floats (S/kernels/attention.hpp:147-161): per-split
+ * (max, sum, output) partials instead of a whole score row per head. */
+uint64_t syn_hip_attention_scratch_bytes(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                         uint32_t max_ctx, uint32_t max_batch);
+
+/* session::execute(op_attention) (S/graph/session.hpp:348-374): store the
+ * run's n K, V rows at positions pos..pos+n-1, rounded to binary16 (kv_append,
+ * S/kernels/attention.hpp:165-175), then for every token i and query head h,
+ * out_i,h = softmax_t(scale * fp16(q_i,h) . K_t,g) V_t,g over t = 0..pos+i,
+ * g = h / (n_heads / n_kv_heads) (attend_group, S/kernels/attention.hpp:185-244;
+ * attention, :254-269). Softmax and accumulation in f32, f32 output. */
+int syn_hip_attention(syn_arena* arena, const syn_attn_desc* desc);
+
+/* The attend half only: the cache already holds rows 0..pos+n-1 (desc's
+ * k_offset and v_offset are ignored). */
+int syn_hip_attend(syn_arena* arena, const syn_attn_desc* desc);
+
+/* kv_append for n rows (S/kernels/attention.hpp:165-175, driven as
+ * S/graph/session.hpp:354-356): rows pos0..pos0+n-1 of K and V^T <- fp16 of
+ * the n rows at k_rows / v_rows (type kv_dtype). */
+int syn_hip_kv_append(syn_arena* arena, const syn_kv_desc* cache, uint64_t k_rows, uint64_t v_rows, uint32_t n,
+                      uint32_t pos0, uint32_t kv_dtype);
+
+/* ---- ragged batched decode ----------------------------------------------
+ * No reference counterpart: the reference decodes one sequence per session
+ * (S/graph/session.hpp:34-43), so a batch is n_seqs separate attention()
+ * calls. Here each sequence has its own KV state in the arena and attends
+ * its one query row to its cached rows 0..pos (already appended). */
+typedef struct syn_seq_desc {
+    syn_kv_desc cache;
+    uint64_t q_offset;   /* one row of n_heads*head_dim, type q_dtype */
+    uint64_t out_offset; /* one row of n_heads*head_dim f32 */
+    uint32_t pos;        /* attends rows 0..pos */
+    uint32_t reserved;
+} syn_seq_desc;
+
+uint64_t syn_hip_attend_batch_scratch_bytes(const syn_seq_desc* seqs, uint32_t n_seqs, uint32_t n_heads);
+int syn_hip_attend_batch(syn_arena* arena, const syn_seq_desc* seqs, uint32_t n_seqs, uint32_t n_heads,
+                         float scale, uint32_t q_dtype, uint64_t scratch_offset, uint64_t scratch_bytes);
+
+/* ---- bidirectional self-attention (image encoders) ----------------------
+ * session::execute(op_self_attention) (S/graph/session.hpp:409-449) with
+ * self_attend_head's math (S/kernels/attention.hpp:460-486): for every row i
+ * and head h, out_i,h = softmax_j(scale * q_i,h . k_j,h) v_j,h over j = 0..n-1.
+ * Rows are grouped into `batch` independent images of n rows each (the
+ * reference runs one image per run_rows call, S/models/clip.hpp:405-416).
+ * Operands are rounded to binary16 for the matrix cores; softmax and
+ * accumulation in f32, f32 output. */
+typedef struct syn_self_desc {
+    uint64_t q_offset;   /* batch*n rows of n_heads*head_dim, type in_dtype */
+    uint64_t k_offset;
+    uint64_t v_offset;
+    uint64_t out_offset; /* batch*n rows, f32 */
+    uint32_t n;          /* rows per image, >= 1 */
+    uint32_t batch;      /* images, >= 1 */
+    uint32_t n_heads;
+    uint32_t head_dim;
+    float scale;
+    uint32_t in_dtype;   /* SYN_F32 or SYN_F16 */
+} syn_self_desc;
+
+int syn_hip_self_attention(syn_arena* arena, const syn_self_desc* desc);
+
+/* ---- RoPE ---------------------------------------------------------------
+ * op_rope (S/graph/session.hpp:337-342) with rope's math
+ * (S/kernels/attention.hpp:89-129): row i of n rows of `size` floats is
+ * rotated by position pos+i, theta_i = pos * theta_scale^i / freq_factor[i]
+ * built by repeated f32 multiplication; mode 0 pairs (x[2i], x[2i+1]),
+ * mode 1 (neox) pairs (x[i], x[i+hd/2]). YaRN scaling when ext_factor != 0. */
+typedef struct syn_rope_desc {
+    uint64_t in_offset;           /* n rows of size f32 */
+    uint64_t out_offset;          /* n rows of size f32; may not alias in */
+    uint64_t freq_factors_offset; /* head_dim/2 f32, or UINT64_MAX for none */
+    uint32_t n;
+    uint32_t size;                /* a multiple of head_dim */
+    uint32_t head_dim;            /* even */
+    uint32_t pos;
+    float theta_scale;            /* base^(-2/head_dim) */
+    uint32_t mode;                /* 0 normal, 1 neox */
+    float freq_scale, ext_factor, attn_factor, corr_low, corr_high;
+} syn_rope_desc;
+
+int syn_hip_rope(syn_arena* arena, const syn_rope_desc* desc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYNAPSE_HIP_H */

@@ -1,0 +1,114 @@
+"""Builds the gfx950 attention library (and, for tests, the CPU oracle and the
+C++ host tests) in-tree.
+
+    python -m synapse_amd.build            # library + oracle + host tests
+    python -m synapse_amd.build --lib      # library only
+
+Outputs (git-ignored, but shipped to the GPU box with the tree):
+    synapse_amd/libsynapse_hip.so          the C ABI of include/synapse_hip.h
+    oracle/liboracle.so                    CPU oracle (test infrastructure)
+    oracle/_ref/libref_half.so             the reference's own binary16 code
+    tests/cpp/_bin/*                       C++ host tests
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+PKG = ROOT / "synapse_amd"
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libsynapse_hip.so"
+HOST_INC = PKG / "host"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++20",
+    "-fPIC",
+    "-Wall",
+    "-Werror",
+    # Packed-FP32 instructions stay off on this pool (wrong results seen).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+HIP_SOURCES = ["kv_append.hip", "decode.hip", "flash.hip", "generic.hip", "rope.hip", "capi.hip"]
+
+
+def _run(cmd: list[str], cwd: pathlib.Path | None = None) -> None:
+    proc = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature.
+    out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build failed ({' '.join(cmd)}):\n{out}")
+
+
+def build_library() -> pathlib.Path:
+    BUILD.mkdir(exist_ok=True)
+    objs = []
+
+    def compile_one(src: str) -> pathlib.Path:
+        obj = BUILD / (pathlib.Path(src).stem + ".o")
+        _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        return obj
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(HIP_SOURCES))) as ex:
+        objs = list(ex.map(compile_one, HIP_SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> None:
+    _run(["make", "-s", "-C", str(ROOT / "oracle")])
+
+
+CPP_TESTS = {
+    # name: (source, needs the HIP library)
+    "test_graph": ("tests/cpp/test_graph.cpp", False),
+    "test_session": ("tests/cpp/test_session.cpp", True),
+}
+
+
+def build_host_tests() -> None:
+    out = ROOT / "tests" / "cpp" / "_bin"
+    out.mkdir(parents=True, exist_ok=True)
+    for name, (src, hip) in CPP_TESTS.items():
+        path = ROOT / src
+        if not path.exists():
+            continue
+        cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-Wextra", "-Werror", "-ffp-contract=off",
+               f"-I{HOST_INC}", f"-I{ROOT / 'include'}", f"-I{ROOT / 'oracle'}", str(path), "-o", str(out / name)]
+        if hip:
+            cmd += [f"-L{PKG}", "-lsynapse_hip", f"-Wl,-rpath,{PKG}", f"-L{ROOT / 'oracle'}", "-loracle",
+                    f"-Wl,-rpath,{ROOT / 'oracle'}", "-pthread"]
+        _run(cmd)
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--lib", action="store_true", help="build the HIP library only")
+    args = ap.parse_args(argv)
+    if not shutil.which(HIPCC) and not pathlib.Path(HIPCC).exists():
+        print(f"hipcc not found at {HIPCC}", file=sys.stderr)
+        return 1
+    build_library()
+    print(f"built {LIB.relative_to(ROOT)}")
+    if not args.lib:
+        build_oracle()
+        print("built oracle/liboracle.so")
+        build_host_tests()
+        print("built tests/cpp/_bin")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

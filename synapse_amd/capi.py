@@ -1,0 +1,193 @@
+"""ctypes binding of the C ABI in include/synapse_hip.h.
+
+The library must have been built (python -m synapse_amd.build); loading fails
+loudly otherwise -- there is no fallback path. Every call returning a status
+raises SynHipError on a non-zero status, with the library's detail message.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+LIB_PATH = ROOT / "libsynapse_hip.so"
+
+SYN_F32 = 0
+SYN_F16 = 1
+NO_OFFSET = (1 << 64) - 1
+
+u64, u32, f32, i32 = ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float, ctypes.c_int
+
+
+class KvDesc(ctypes.Structure):
+    _fields_ = [("k_offset", u64), ("v_offset", u64), ("max_ctx", u32), ("n_kv_heads", u32),
+                ("head_dim", u32), ("ctx_stride", u32)]
+
+
+class AttnDesc(ctypes.Structure):
+    _fields_ = [("cache", KvDesc), ("q_offset", u64), ("k_offset", u64), ("v_offset", u64),
+                ("out_offset", u64), ("scratch_offset", u64), ("scratch_bytes", u64), ("n_heads", u32),
+                ("pos", u32), ("n", u32), ("scale", f32), ("q_dtype", u32), ("kv_dtype", u32)]
+
+
+class SeqDesc(ctypes.Structure):
+    _fields_ = [("cache", KvDesc), ("q_offset", u64), ("out_offset", u64), ("pos", u32), ("reserved", u32)]
+
+
+class SelfDesc(ctypes.Structure):
+    _fields_ = [("q_offset", u64), ("k_offset", u64), ("v_offset", u64), ("out_offset", u64), ("n", u32),
+                ("batch", u32), ("n_heads", u32), ("head_dim", u32), ("scale", f32), ("in_dtype", u32)]
+
+
+class RopeDesc(ctypes.Structure):
+    _fields_ = [("in_offset", u64), ("out_offset", u64), ("freq_factors_offset", u64), ("n", u32), ("size", u32),
+                ("head_dim", u32), ("pos", u32), ("theta_scale", f32), ("mode", u32), ("freq_scale", f32),
+                ("ext_factor", f32), ("attn_factor", f32), ("corr_low", f32), ("corr_high", f32)]
+
+
+# name -> (restype, argtypes); every symbol include/synapse_hip.h declares.
+SIGNATURES = {
+    "syn_hip_error_string": (ctypes.c_char_p, [i32]),
+    "syn_hip_last_error": (ctypes.c_char_p, []),
+    "syn_hip_arena_create": (i32, [ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]),
+    "syn_hip_arena_destroy": (i32, [ctypes.c_void_p]),
+    "syn_hip_arena_bytes": (ctypes.c_size_t, [ctypes.c_void_p]),
+    "syn_hip_arena_stream": (ctypes.c_void_p, [ctypes.c_void_p]),
+    "syn_hip_upload": (i32, [ctypes.c_void_p, u64, ctypes.c_void_p, ctypes.c_size_t]),
+    "syn_hip_download": (i32, [ctypes.c_void_p, u64, ctypes.c_void_p, ctypes.c_size_t]),
+    "syn_hip_fill": (i32, [ctypes.c_void_p, u64, i32, ctypes.c_size_t]),
+    "syn_hip_copy": (i32, [ctypes.c_void_p, u64, u64, ctypes.c_size_t]),
+    "syn_hip_synchronize": (i32, [ctypes.c_void_p]),
+    "syn_hip_kv_ctx_stride": (u32, [u32]),
+    "syn_hip_kv_state_bytes": (u64, [u32, u32, u32]),
+    "syn_hip_attention_scratch_bytes": (u64, [u32, u32, u32, u32, u32]),
+    "syn_hip_attention": (i32, [ctypes.c_void_p, ctypes.POINTER(AttnDesc)]),
+    "syn_hip_attend": (i32, [ctypes.c_void_p, ctypes.POINTER(AttnDesc)]),
+    "syn_hip_kv_append": (i32, [ctypes.c_void_p, ctypes.POINTER(KvDesc), u64, u64, u32, u32, u32]),
+    "syn_hip_attend_batch_scratch_bytes": (u64, [ctypes.POINTER(SeqDesc), u32, u32]),
+    "syn_hip_attend_batch": (i32, [ctypes.c_void_p, ctypes.POINTER(SeqDesc), u32, u32, f32, u32, u64, u64]),
+    "syn_hip_self_attention": (i32, [ctypes.c_void_p, ctypes.POINTER(SelfDesc)]),
+    "syn_hip_rope": (i32, [ctypes.c_void_p, ctypes.POINTER(RopeDesc)]),
+}
+
+_lib = None
+
+
+class SynHipError(RuntimeError):
+    def __init__(self, code: int, detail: str):
+        super().__init__(f"synapse_hip error {code}: {detail}")
+        self.code = code
+        self.detail = detail
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m synapse_amd.build`")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        detail = lib().syn_hip_last_error().decode()
+        raise SynHipError(status, detail or lib().syn_hip_error_string(status).decode())
+
+
+def align(x: int, a: int = 256) -> int:
+    return (x + a - 1) // a * a
+
+
+class Arena:
+    """One device arena (one hipMalloc) with a bump allocator for offsets."""
+
+    def __init__(self, nbytes: int):
+        self.handle = ctypes.c_void_p()
+        check(lib().syn_hip_arena_create(nbytes, ctypes.byref(self.handle)))
+        self.nbytes = nbytes
+        self.top = 0
+
+    def alloc(self, nbytes: int, alignment: int = 256) -> int:
+        off = align(self.top, alignment)
+        if off + nbytes > self.nbytes:
+            raise MemoryError(f"arena of {self.nbytes} bytes cannot hold {nbytes} more at {off}")
+        self.top = off + nbytes
+        return off
+
+    def put(self, array: np.ndarray, alignment: int = 256) -> int:
+        a = np.ascontiguousarray(array)
+        off = self.alloc(a.nbytes, alignment)
+        self.upload(off, a)
+        return off
+
+    def upload(self, offset: int, array: np.ndarray) -> None:
+        a = np.ascontiguousarray(array)
+        check(lib().syn_hip_upload(self.handle, offset, a.ctypes.data, a.nbytes))
+
+    def download(self, offset: int, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        check(lib().syn_hip_download(self.handle, offset, out.ctypes.data, out.nbytes))
+        return out
+
+    def fill(self, offset: int, value: int, nbytes: int) -> None:
+        check(lib().syn_hip_fill(self.handle, offset, value, nbytes))
+
+    def sync(self) -> None:
+        check(lib().syn_hip_synchronize(self.handle))
+
+    @property
+    def stream(self) -> int:
+        return lib().syn_hip_arena_stream(self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().syn_hip_arena_destroy(self.handle))
+            self.handle = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def kv_state(arena: Arena, max_ctx: int, n_kv: int, hd: int) -> KvDesc:
+    """Places one KV state in the arena (K block, then V^T block)."""
+    stride = lib().syn_hip_kv_ctx_stride(max_ctx)
+    k_bytes = align(max_ctx * n_kv * hd * 2)
+    base = arena.alloc(lib().syn_hip_kv_state_bytes(max_ctx, n_kv, hd))
+    return KvDesc(k_offset=base, v_offset=base + k_bytes, max_ctx=max_ctx, n_kv_heads=n_kv, head_dim=hd,
+                  ctx_stride=stride)
+
+
+def kv_state_bytes(max_ctx: int, n_kv: int, hd: int) -> int:
+    return int(lib().syn_hip_kv_state_bytes(max_ctx, n_kv, hd))
+
+
+def upload_cache(arena: Arena, c: KvDesc, k_rows16: np.ndarray, v_rows16: np.ndarray) -> None:
+    """Writes binary16 K, V rows [L][n_kv*hd] (uint16 bit patterns) straight
+    into a state's K and V^T blocks (positions 0..L-1)."""
+    L = k_rows16.shape[0]
+    row = c.n_kv_heads * c.head_dim
+    assert k_rows16.shape == (L, row) and v_rows16.shape == (L, row) and L <= c.max_ctx
+    arena.upload(c.k_offset, k_rows16.astype(np.uint16))
+    vt = np.zeros((row, c.ctx_stride), dtype=np.uint16)
+    vt[:, :L] = v_rows16.T
+    arena.upload(c.v_offset, vt)
+
+
+def download_cache(arena: Arena, c: KvDesc, L: int) -> tuple[np.ndarray, np.ndarray]:
+    """Rows 0..L-1 of a state's K and V, as [L][n_kv*hd] uint16 (V untransposed)."""
+    row = c.n_kv_heads * c.head_dim
+    k = arena.download(c.k_offset, (c.max_ctx, row), np.uint16)[:L]
+    vt = arena.download(c.v_offset, (row, c.ctx_stride), np.uint16)
+    return k, np.ascontiguousarray(vt[:, :L].T)

@@ -1,0 +1,705 @@
+// capi.hip — the extern "C" boundary (include/synapse_hip.h).
+//
+// Every entry point checks its descriptor on the host -- shapes, alignment,
+// and that every byte a kernel may touch lies inside the arena -- before it
+// queues anything, so a bad descriptor is an error code, never a GPU fault.
+// Nothing here throws; nothing here allocates after syn_hip_arena_create.
+
+#include "../../include/synapse_hip.h"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+struct syn_arena {
+    char* base = nullptr;          // user bytes, then the control block
+    std::size_t bytes = 0;         // user bytes
+    uint32_t* counters = nullptr;  // decode merge counters (control block)
+    hipStream_t stream = nullptr;
+    int device = 0;
+};
+
+namespace {
+
+constexpr uint32_t n_counters = 16384;
+constexpr std::size_t control_bytes = n_counters * sizeof(uint32_t);
+constexpr uint64_t no_offset = ~uint64_t{0};
+
+thread_local char last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(last_error, sizeof last_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) {
+        return SYN_HIP_OK;
+    }
+    return fail(static_cast<int>(e), "%s: %s", what, hipGetErrorString(e));
+}
+
+// [offset, offset + bytes) inside the arena, without wrapping.
+bool in_arena(const syn_arena* a, uint64_t offset, uint64_t bytes) {
+    return offset <= a->bytes && bytes <= a->bytes - offset;
+}
+
+bool aligned(uint64_t offset, uint64_t to) {
+    return offset % to == 0;
+}
+
+std::size_t dtype_size(uint32_t t) {
+    return t == SYN_F16 ? 2 : 4;
+}
+
+bool dtype_ok(uint32_t t) {
+    return t == SYN_F32 || t == SYN_F16;
+}
+
+int check_arena(const syn_arena* a) {
+    if (a == nullptr || a->base == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null arena");
+    }
+    return SYN_HIP_OK;
+}
+
+int check_range(const syn_arena* a, uint64_t offset, uint64_t bytes, uint64_t align, const char* what) {
+    if (!in_arena(a, offset, bytes)) {
+        return fail(SYN_HIP_ERANGE, "%s: [%llu, +%llu) outside the arena of %zu bytes", what,
+                    static_cast<unsigned long long>(offset), static_cast<unsigned long long>(bytes), a->bytes);
+    }
+    if (!aligned(offset, align)) {
+        return fail(SYN_HIP_EINVAL, "%s: offset %llu not %llu-byte aligned", what,
+                    static_cast<unsigned long long>(offset), static_cast<unsigned long long>(align));
+    }
+    return SYN_HIP_OK;
+}
+
+uint32_t ctx_stride_of(uint32_t max_ctx) {
+    return (max_ctx + 63u) / 64u * 64u;
+}
+
+uint64_t align256(uint64_t x) {
+    return (x + 255u) / 256u * 256u;
+}
+
+// A KV state: shape limits of kv_cache (S/graph/graph.hpp:698-719) and the
+// byte ranges of both blocks.
+int check_cache(const syn_arena* a, const syn_kv_desc& c) {
+    if (c.max_ctx == 0 || c.n_kv_heads == 0 || c.head_dim == 0 || c.head_dim > 256 || c.head_dim % 2 != 0) {
+        return fail(SYN_HIP_EINVAL, "kv cache: max_ctx %u, n_kv_heads %u, head_dim %u", c.max_ctx, c.n_kv_heads,
+                    c.head_dim);
+    }
+    if (c.ctx_stride < c.max_ctx || c.ctx_stride % 8 != 0) {
+        return fail(SYN_HIP_EINVAL, "kv cache: ctx_stride %u for max_ctx %u (want a multiple of 8 >= max_ctx)",
+                    c.ctx_stride, c.max_ctx);
+    }
+    const uint64_t row = uint64_t{c.n_kv_heads} * c.head_dim;
+    if (int e = check_range(a, c.k_offset, uint64_t{c.max_ctx} * row * 2, 16, "kv cache K")) {
+        return e;
+    }
+    if (int e = check_range(a, c.v_offset, row * c.ctx_stride * 2, 16, "kv cache V^T")) {
+        return e;
+    }
+    return SYN_HIP_OK;
+}
+
+syn::kv_layout layout_of(syn_arena* a, const syn_kv_desc& c) {
+    return syn::kv_layout{reinterpret_cast<_Float16*>(a->base + c.k_offset),
+                          reinterpret_cast<_Float16*>(a->base + c.v_offset), c.max_ctx, c.n_kv_heads, c.head_dim,
+                          c.ctx_stride};
+}
+
+// Matrix-core kernels need 16-byte operand chunks: head_dim a multiple of 8.
+bool fast_shape(uint32_t hd) {
+    return hd % 8 == 0;
+}
+
+uint64_t decode_scratch_bytes(uint32_t splits, uint32_t n_kv, uint32_t group, uint32_t hd) {
+    return uint64_t{splits} * n_kv * syn::decode_split_floats(group, hd) * sizeof(float);
+}
+
+// One decode launch over seqs[0..n): fills the argument block, checks the
+// scratch, launches.
+int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n_kv, uint32_t hd, uint32_t group,
+               float scale, uint32_t q_dtype, uint64_t scratch_offset, uint64_t scratch_bytes) {
+    syn::decode_args args{};
+    uint64_t positions = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        positions += seqs[i].len;
+    }
+    const uint32_t chunk = syn::decode_choose_chunk(positions, n_kv);
+    uint32_t splits = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        args.seq[i] = seqs[i];
+        args.seq[i].block0 = splits;
+        args.seq[i].n_splits = (seqs[i].len + chunk - 1) / chunk;
+        splits += args.seq[i].n_splits;
+    }
+    args.n_seqs = n;
+    args.n_kv = n_kv;
+    args.hd = hd;
+    args.group = group;
+    args.row = n_kv * hd;
+    args.chunk = chunk;
+    args.counter0 = 0;
+    args.scale_log2e = scale * syn::log2e;
+    args.counters = a->counters;
+    bool any_split = false;
+    for (uint32_t i = 0; i < n; ++i) {
+        any_split = any_split || args.seq[i].n_splits > 1;
+    }
+    if (any_split) {
+        const uint64_t need = decode_scratch_bytes(splits, n_kv, group, hd);
+        if (need > scratch_bytes) {
+            return fail(SYN_HIP_EINVAL, "decode: scratch of %llu bytes, %llu needed",
+                        static_cast<unsigned long long>(scratch_bytes), static_cast<unsigned long long>(need));
+        }
+        if (int e = check_range(a, scratch_offset, need, 16, "decode scratch")) {
+            return e;
+        }
+        float* part = reinterpret_cast<float*>(a->base + scratch_offset);
+        args.part_o = part;
+        args.part_ml = part + uint64_t{splits} * n_kv * group * hd;
+    }
+    if (uint64_t{n} * n_kv > n_counters) {
+        return fail(SYN_HIP_EUNSUPPORTED, "decode: %u sequences x %u KV heads exceed %u merge counters", n, n_kv,
+                    n_counters);
+    }
+    return hip_status(syn::launch_decode(args, splits, q_dtype, a->stream), "decode launch");
+}
+
+int check_attn(const syn_arena* a, const syn_attn_desc* d, bool with_new_rows) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (int e = check_cache(a, d->cache)) {
+        return e;
+    }
+    const syn_kv_desc& c = d->cache;
+    if (d->n_heads == 0 || d->n_heads % c.n_kv_heads != 0) {
+        return fail(SYN_HIP_EINVAL, "attention: %u query heads on %u KV heads", d->n_heads, c.n_kv_heads);
+    }
+    if (!(std::isfinite(d->scale) && d->scale > 0.0f)) {
+        return fail(SYN_HIP_EINVAL, "attention: scale %g (want finite and > 0)", static_cast<double>(d->scale));
+    }
+    if (d->n == 0 || uint64_t{d->pos} + d->n > c.max_ctx) {
+        return fail(SYN_HIP_EINVAL, "attention: run of %u at position %u on a cache of %u", d->n, d->pos, c.max_ctx);
+    }
+    if (!dtype_ok(d->q_dtype) || !dtype_ok(d->kv_dtype)) {
+        return fail(SYN_HIP_EINVAL, "attention: dtypes %u, %u", d->q_dtype, d->kv_dtype);
+    }
+    const uint64_t qsize = uint64_t{d->n_heads} * c.head_dim;
+    const uint64_t row = uint64_t{c.n_kv_heads} * c.head_dim;
+    if (int e = check_range(a, d->q_offset, d->n * qsize * dtype_size(d->q_dtype), 16, "attention q")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, d->n * qsize * 4, 16, "attention out")) {
+        return e;
+    }
+    if (with_new_rows) {
+        if (int e = check_range(a, d->k_offset, d->n * row * dtype_size(d->kv_dtype), 16, "attention k")) {
+            return e;
+        }
+        if (int e = check_range(a, d->v_offset, d->n * row * dtype_size(d->kv_dtype), 16, "attention v")) {
+            return e;
+        }
+    }
+    return SYN_HIP_OK;
+}
+
+syn::flash_args flash_of(syn_arena* a, const syn_attn_desc* d) {
+    const syn_kv_desc& c = d->cache;
+    syn::flash_args f{};
+    f.q = a->base + d->q_offset;
+    f.out = reinterpret_cast<float*>(a->base + d->out_offset);
+    f.k = reinterpret_cast<const _Float16*>(a->base + c.k_offset);
+    f.vt = reinterpret_cast<const _Float16*>(a->base + c.v_offset);
+    f.n = d->n;
+    f.batch = 1;
+    f.pos = d->pos;
+    f.kv_len = d->pos + d->n;
+    f.n_heads = d->n_heads;
+    f.n_kv = c.n_kv_heads;
+    f.hd = c.head_dim;
+    f.group = d->n_heads / c.n_kv_heads;
+    f.q_row = d->n_heads * c.head_dim;
+    f.row = c.n_kv_heads * c.head_dim;
+    f.ctx_stride = c.ctx_stride;
+    f.scale_log2e = d->scale * syn::log2e;
+    return f;
+}
+
+int attend_checked(syn_arena* a, const syn_attn_desc* d) {
+    const syn_kv_desc& c = d->cache;
+    const uint32_t group = d->n_heads / c.n_kv_heads;
+    if (d->n == 1 && fast_shape(c.head_dim) && group <= 16) {
+        syn::decode_seq s{};
+        s.q = a->base + d->q_offset;
+        s.out = reinterpret_cast<float*>(a->base + d->out_offset);
+        s.k = reinterpret_cast<const _Float16*>(a->base + c.k_offset);
+        s.vt = reinterpret_cast<const _Float16*>(a->base + c.v_offset);
+        s.len = d->pos + 1;
+        s.ctx_stride = c.ctx_stride;
+        return run_decode(a, &s, 1, c.n_kv_heads, c.head_dim, group, d->scale, d->q_dtype, d->scratch_offset,
+                          d->scratch_bytes);
+    }
+    const syn::flash_args f = flash_of(a, d);
+    if (fast_shape(c.head_dim)) {
+        return hip_status(syn::launch_prefill(f, d->q_dtype, a->stream), "prefill launch");
+    }
+    return hip_status(syn::launch_generic_causal(f, d->q_dtype, a->stream), "generic causal launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* syn_hip_error_string(int status) {
+    switch (status) {
+    case SYN_HIP_OK:
+        return "ok";
+    case SYN_HIP_EINVAL:
+        return "invalid argument";
+    case SYN_HIP_ERANGE:
+        return "offset outside the arena";
+    case SYN_HIP_EUNSUPPORTED:
+        return "unsupported shape";
+    case SYN_HIP_ENOMEM:
+        return "device allocation failed";
+    case SYN_HIP_ENODEV:
+        return "no gfx950 device";
+    default:
+        return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown error";
+    }
+}
+
+const char* syn_hip_last_error(void) {
+    return last_error;
+}
+
+int syn_hip_arena_create(size_t bytes, syn_arena** out) {
+    if (out == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null output pointer");
+    }
+    *out = nullptr;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        return fail(SYN_HIP_ENODEV, "no HIP device");
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        return fail(SYN_HIP_ENODEV, "hipGetDeviceProperties failed");
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        return fail(SYN_HIP_ENODEV, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
+    }
+    const std::size_t user = align256(bytes);
+    if (user < bytes || user > SIZE_MAX - control_bytes) {
+        return fail(SYN_HIP_EINVAL, "arena of %zu bytes", bytes);
+    }
+    auto* a = new (std::nothrow) syn_arena;
+    if (a == nullptr) {
+        return fail(SYN_HIP_ENOMEM, "host allocation failed");
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, user + control_bytes) != hipSuccess) {
+        delete a;
+        return fail(SYN_HIP_ENOMEM, "hipMalloc of %zu bytes failed", user + control_bytes);
+    }
+    a->base = static_cast<char*>(p);
+    a->bytes = bytes;
+    a->counters = reinterpret_cast<uint32_t*>(a->base + user);
+    a->device = device;
+    if (hipStreamCreateWithFlags(&a->stream, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipFree(p);
+        delete a;
+        return fail(SYN_HIP_ENOMEM, "hipStreamCreate failed");
+    }
+    if (int e = hip_status(hipMemsetAsync(a->counters, 0, control_bytes, a->stream), "control block")) {
+        (void)hipStreamDestroy(a->stream);
+        (void)hipFree(p);
+        delete a;
+        return e;
+    }
+    if (int e = hip_status(hipStreamSynchronize(a->stream), "arena init")) {
+        (void)hipStreamDestroy(a->stream);
+        (void)hipFree(p);
+        delete a;
+        return e;
+    }
+    *out = a;
+    return SYN_HIP_OK;
+}
+
+int syn_hip_arena_destroy(syn_arena* a) {
+    if (a == nullptr) {
+        return SYN_HIP_OK;
+    }
+    int e = hip_status(hipStreamSynchronize(a->stream), "destroy sync");
+    (void)hipStreamDestroy(a->stream);
+    (void)hipFree(a->base);
+    delete a;
+    return e;
+}
+
+size_t syn_hip_arena_bytes(const syn_arena* a) {
+    return a ? a->bytes : 0;
+}
+
+void* syn_hip_arena_stream(syn_arena* a) {
+    return a ? static_cast<void*>(a->stream) : nullptr;
+}
+
+int syn_hip_upload(syn_arena* a, uint64_t offset, const void* host, size_t bytes) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (int e = check_range(a, offset, bytes, 1, "upload")) {
+        return e;
+    }
+    if (bytes == 0) {
+        return SYN_HIP_OK;
+    }
+    if (host == nullptr) {
+        return fail(SYN_HIP_EINVAL, "upload: null host pointer");
+    }
+    return hip_status(hipMemcpyAsync(a->base + offset, host, bytes, hipMemcpyHostToDevice, a->stream), "upload");
+}
+
+int syn_hip_download(syn_arena* a, uint64_t offset, void* host, size_t bytes) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (int e = check_range(a, offset, bytes, 1, "download")) {
+        return e;
+    }
+    if (bytes == 0) {
+        return SYN_HIP_OK;
+    }
+    if (host == nullptr) {
+        return fail(SYN_HIP_EINVAL, "download: null host pointer");
+    }
+    if (int e = hip_status(hipMemcpyAsync(host, a->base + offset, bytes, hipMemcpyDeviceToHost, a->stream),
+                           "download")) {
+        return e;
+    }
+    return hip_status(hipStreamSynchronize(a->stream), "download sync");
+}
+
+int syn_hip_fill(syn_arena* a, uint64_t offset, int value, size_t bytes) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (int e = check_range(a, offset, bytes, 1, "fill")) {
+        return e;
+    }
+    if (bytes == 0) {
+        return SYN_HIP_OK;
+    }
+    return hip_status(hipMemsetAsync(a->base + offset, value, bytes, a->stream), "fill");
+}
+
+int syn_hip_copy(syn_arena* a, uint64_t dst, uint64_t src, size_t bytes) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (int e = check_range(a, dst, bytes, 1, "copy dst")) {
+        return e;
+    }
+    if (int e = check_range(a, src, bytes, 1, "copy src")) {
+        return e;
+    }
+    if (bytes == 0) {
+        return SYN_HIP_OK;
+    }
+    return hip_status(hipMemcpyAsync(a->base + dst, a->base + src, bytes, hipMemcpyDeviceToDevice, a->stream),
+                      "copy");
+}
+
+int syn_hip_synchronize(syn_arena* a) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    return hip_status(hipStreamSynchronize(a->stream), "synchronize");
+}
+
+uint32_t syn_hip_kv_ctx_stride(uint32_t max_ctx) {
+    return ctx_stride_of(max_ctx);
+}
+
+uint64_t syn_hip_kv_state_bytes(uint32_t max_ctx, uint32_t n_kv_heads, uint32_t head_dim) {
+    const uint64_t row = uint64_t{n_kv_heads} * head_dim;
+    return align256(uint64_t{max_ctx} * row * 2) + align256(row * ctx_stride_of(max_ctx) * 2);
+}
+
+uint64_t syn_hip_attention_scratch_bytes(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t max_ctx,
+                                         uint32_t max_batch) {
+    (void)max_batch;  // runs of more than one token use the flash kernel, which needs none
+    if (n_kv_heads == 0 || n_heads % n_kv_heads != 0) {
+        return 0;
+    }
+    const uint32_t splits = (max_ctx + syn::decode_chunk_unit - 1) / syn::decode_chunk_unit;
+    return align256(decode_scratch_bytes(splits, n_kv_heads, n_heads / n_kv_heads, head_dim));
+}
+
+int syn_hip_kv_append(syn_arena* a, const syn_kv_desc* cache, uint64_t k_rows, uint64_t v_rows, uint32_t n,
+                      uint32_t pos0, uint32_t kv_dtype) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (cache == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null cache descriptor");
+    }
+    if (int e = check_cache(a, *cache)) {
+        return e;
+    }
+    if (!dtype_ok(kv_dtype)) {
+        return fail(SYN_HIP_EINVAL, "kv_append: dtype %u", kv_dtype);
+    }
+    if (n == 0) {
+        return SYN_HIP_OK;
+    }
+    if (uint64_t{pos0} + n > cache->max_ctx) {
+        return fail(SYN_HIP_EINVAL, "kv_append: rows %u..%u on a cache of %u", pos0, pos0 + n - 1, cache->max_ctx);
+    }
+    const uint64_t bytes = uint64_t{n} * cache->n_kv_heads * cache->head_dim * dtype_size(kv_dtype);
+    if (int e = check_range(a, k_rows, bytes, dtype_size(kv_dtype), "kv_append k")) {
+        return e;
+    }
+    if (int e = check_range(a, v_rows, bytes, dtype_size(kv_dtype), "kv_append v")) {
+        return e;
+    }
+    return hip_status(syn::launch_kv_append(layout_of(a, *cache), a->base + k_rows, a->base + v_rows, n, pos0,
+                                            kv_dtype, a->stream),
+                      "kv_append launch");
+}
+
+int syn_hip_attention(syn_arena* a, const syn_attn_desc* d) {
+    if (int e = check_attn(a, d, true)) {
+        return e;
+    }
+    if (int e = syn_hip_kv_append(a, &d->cache, d->k_offset, d->v_offset, d->n, d->pos, d->kv_dtype)) {
+        return e;
+    }
+    return attend_checked(a, d);
+}
+
+int syn_hip_attend(syn_arena* a, const syn_attn_desc* d) {
+    if (int e = check_attn(a, d, false)) {
+        return e;
+    }
+    return attend_checked(a, d);
+}
+
+uint64_t syn_hip_attend_batch_scratch_bytes(const syn_seq_desc* seqs, uint32_t n_seqs, uint32_t n_heads) {
+    if (seqs == nullptr || n_seqs == 0 || seqs[0].cache.n_kv_heads == 0) {
+        return 0;
+    }
+    const uint32_t n_kv = seqs[0].cache.n_kv_heads;
+    const uint32_t hd = seqs[0].cache.head_dim;
+    uint64_t worst = 0;
+    for (uint32_t b0 = 0; b0 < n_seqs; b0 += syn::decode_max_seqs) {
+        const uint32_t nb = std::min(n_seqs - b0, syn::decode_max_seqs);
+        uint64_t positions = 0;
+        for (uint32_t i = 0; i < nb; ++i) {
+            positions += uint64_t{seqs[b0 + i].pos} + 1;
+        }
+        const uint32_t chunk = syn::decode_choose_chunk(positions, n_kv);
+        uint64_t splits = 0;
+        for (uint32_t i = 0; i < nb; ++i) {
+            splits += (uint64_t{seqs[b0 + i].pos} + chunk) / chunk;
+        }
+        worst = std::max(worst, splits * n_kv * syn::decode_split_floats(n_heads / n_kv, hd) * sizeof(float));
+    }
+    return align256(worst);
+}
+
+int syn_hip_attend_batch(syn_arena* a, const syn_seq_desc* seqs, uint32_t n_seqs, uint32_t n_heads, float scale,
+                         uint32_t q_dtype, uint64_t scratch_offset, uint64_t scratch_bytes) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (seqs == nullptr || n_seqs == 0) {
+        return fail(SYN_HIP_EINVAL, "attend_batch: no sequences");
+    }
+    if (!(std::isfinite(scale) && scale > 0.0f) || !dtype_ok(q_dtype)) {
+        return fail(SYN_HIP_EINVAL, "attend_batch: scale %g, dtype %u", static_cast<double>(scale), q_dtype);
+    }
+    const uint32_t n_kv = seqs[0].cache.n_kv_heads;
+    const uint32_t hd = seqs[0].cache.head_dim;
+    for (uint32_t i = 0; i < n_seqs; ++i) {
+        const syn_seq_desc& s = seqs[i];
+        if (int e = check_cache(a, s.cache)) {
+            return e;
+        }
+        if (s.cache.n_kv_heads != n_kv || s.cache.head_dim != hd) {
+            return fail(SYN_HIP_EINVAL, "attend_batch: sequence %u has a different head layout", i);
+        }
+        if (s.pos >= s.cache.max_ctx) {
+            return fail(SYN_HIP_EINVAL, "attend_batch: sequence %u at position %u of %u", i, s.pos,
+                        s.cache.max_ctx);
+        }
+        const uint64_t qsize = uint64_t{n_heads} * hd;
+        if (int e = check_range(a, s.q_offset, qsize * dtype_size(q_dtype), 16, "attend_batch q")) {
+            return e;
+        }
+        if (int e = check_range(a, s.out_offset, qsize * 4, 16, "attend_batch out")) {
+            return e;
+        }
+    }
+    if (n_heads == 0 || n_heads % n_kv != 0) {
+        return fail(SYN_HIP_EINVAL, "attend_batch: %u query heads on %u KV heads", n_heads, n_kv);
+    }
+    const uint32_t group = n_heads / n_kv;
+    if (!fast_shape(hd) || group > 16) {
+        // Shapes outside the split-KV kernel: one causal launch per sequence.
+        for (uint32_t i = 0; i < n_seqs; ++i) {
+            syn_attn_desc d{};
+            d.cache = seqs[i].cache;
+            d.q_offset = seqs[i].q_offset;
+            d.out_offset = seqs[i].out_offset;
+            d.n_heads = n_heads;
+            d.pos = seqs[i].pos;
+            d.n = 1;
+            d.scale = scale;
+            d.q_dtype = q_dtype;
+            const syn::flash_args f = flash_of(a, &d);
+            if (int e = hip_status(syn::launch_generic_causal(f, q_dtype, a->stream), "generic launch")) {
+                return e;
+            }
+        }
+        return SYN_HIP_OK;
+    }
+    for (uint32_t b0 = 0; b0 < n_seqs; b0 += syn::decode_max_seqs) {
+        const uint32_t nb = std::min(n_seqs - b0, syn::decode_max_seqs);
+        syn::decode_seq ds[syn::decode_max_seqs];
+        for (uint32_t i = 0; i < nb; ++i) {
+            const syn_seq_desc& s = seqs[b0 + i];
+            ds[i] = syn::decode_seq{};
+            ds[i].q = a->base + s.q_offset;
+            ds[i].out = reinterpret_cast<float*>(a->base + s.out_offset);
+            ds[i].k = reinterpret_cast<const _Float16*>(a->base + s.cache.k_offset);
+            ds[i].vt = reinterpret_cast<const _Float16*>(a->base + s.cache.v_offset);
+            ds[i].len = s.pos + 1;
+            ds[i].ctx_stride = s.cache.ctx_stride;
+        }
+        if (int e = run_decode(a, ds, nb, n_kv, hd, group, scale, q_dtype, scratch_offset, scratch_bytes)) {
+            return e;
+        }
+    }
+    return SYN_HIP_OK;
+}
+
+int syn_hip_self_attention(syn_arena* a, const syn_self_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->n == 0 || d->batch == 0 || d->n_heads == 0 || d->head_dim == 0 || d->head_dim > 256 ||
+        !dtype_ok(d->in_dtype)) {
+        return fail(SYN_HIP_EINVAL, "self_attention: n %u, batch %u, heads %u, head_dim %u, dtype %u", d->n,
+                    d->batch, d->n_heads, d->head_dim, d->in_dtype);
+    }
+    if (!(std::isfinite(d->scale) && d->scale > 0.0f)) {
+        return fail(SYN_HIP_EINVAL, "self_attention: scale %g", static_cast<double>(d->scale));
+    }
+    const uint64_t rows = uint64_t{d->n} * d->batch;
+    const uint64_t size = uint64_t{d->n_heads} * d->head_dim;
+    const uint64_t in_bytes = rows * size * dtype_size(d->in_dtype);
+    const uint64_t align = fast_shape(d->head_dim) ? 16 : dtype_size(d->in_dtype);
+    if (int e = check_range(a, d->q_offset, in_bytes, align, "self_attention q")) {
+        return e;
+    }
+    if (int e = check_range(a, d->k_offset, in_bytes, align, "self_attention k")) {
+        return e;
+    }
+    if (int e = check_range(a, d->v_offset, in_bytes, align, "self_attention v")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, rows * size * 4, fast_shape(d->head_dim) ? 16 : 4,
+                            "self_attention out")) {
+        return e;
+    }
+    syn::flash_args f{};
+    f.q = a->base + d->q_offset;
+    f.out = reinterpret_cast<float*>(a->base + d->out_offset);
+    f.k_rows = a->base + d->k_offset;
+    f.v_rows = a->base + d->v_offset;
+    f.n = d->n;
+    f.batch = d->batch;
+    f.pos = 0;
+    f.kv_len = d->n;
+    f.n_heads = d->n_heads;
+    f.n_kv = d->n_heads;
+    f.hd = d->head_dim;
+    f.group = 1;
+    f.q_row = static_cast<uint32_t>(size);
+    f.row = static_cast<uint32_t>(size);
+    f.scale_log2e = d->scale * syn::log2e;
+    if (fast_shape(d->head_dim)) {
+        return hip_status(syn::launch_bidirectional(f, d->in_dtype, a->stream), "self_attention launch");
+    }
+    return hip_status(syn::launch_generic_bidirectional(f, d->in_dtype, a->stream), "self_attention launch");
+}
+
+int syn_hip_rope(syn_arena* a, const syn_rope_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->head_dim == 0 || d->head_dim % 2 != 0 || d->size == 0 || d->size % d->head_dim != 0 || d->mode > 1) {
+        return fail(SYN_HIP_EINVAL, "rope: size %u, head_dim %u, mode %u", d->size, d->head_dim, d->mode);
+    }
+    if (d->n == 0) {
+        return SYN_HIP_OK;
+    }
+    const uint64_t bytes = uint64_t{d->n} * d->size * 4;
+    if (int e = check_range(a, d->in_offset, bytes, 4, "rope in")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, bytes, 4, "rope out")) {
+        return e;
+    }
+    if (d->in_offset < d->out_offset + bytes && d->out_offset < d->in_offset + bytes) {
+        return fail(SYN_HIP_EINVAL, "rope: out aliases in");
+    }
+    syn::rope_args r{};
+    r.in = reinterpret_cast<const float*>(a->base + d->in_offset);
+    r.out = reinterpret_cast<float*>(a->base + d->out_offset);
+    if (d->freq_factors_offset != no_offset) {
+        if (int e = check_range(a, d->freq_factors_offset, uint64_t{d->head_dim} / 2 * 4, 4, "rope freq_factors")) {
+            return e;
+        }
+        r.freq_factors = reinterpret_cast<const float*>(a->base + d->freq_factors_offset);
+    }
+    r.n = d->n;
+    r.size = d->size;
+    r.hd = d->head_dim;
+    r.pos = d->pos;
+    r.mode = d->mode;
+    r.theta_scale = d->theta_scale;
+    r.freq_scale = d->freq_scale;
+    r.ext_factor = d->ext_factor;
+    r.attn_factor = d->attn_factor;
+    r.corr_low = d->corr_low;
+    r.corr_high = d->corr_high;
+    return hip_status(syn::launch_rope(r, a->stream), "rope launch");
+}
+
+}  // extern "C"

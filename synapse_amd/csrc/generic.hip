@@ -1,0 +1,108 @@
+// generic.hip — plain f32 attention kernels for the shapes the matrix-core
+// kernels do not take: head_dim not a multiple of 8 (the reference accepts
+// any head_dim <= 256, S/graph/graph.hpp:698-719) and more than 16 query
+// heads per KV head. One wave per (row, head); each lane owns head dims
+// lane, lane+64, ...; online softmax over the keys. Same rounding points as
+// the fast kernels: q and k operands in f16 (exactly the reference's for the
+// causal path), p rounded to f16.
+
+#include "kernels.hpp"
+
+namespace syn {
+
+namespace {
+
+template <bool CAUSAL, bool F16>
+__global__ __launch_bounds__(64) void generic_kernel(const flash_args a) {
+    const int ln = threadIdx.x;
+    const uint32_t i = blockIdx.x;  // query row inside the image
+    const uint32_t h = blockIdx.y;
+    const uint32_t img = blockIdx.z;
+    const uint32_t g = h / a.group;
+    const uint32_t hd = a.hd;
+    const std::size_t row_base = static_cast<std::size_t>(img) * a.n;
+    const float c = a.scale_log2e;
+
+    const auto load = [&](const void* p, std::size_t idx) -> float {
+        if constexpr (F16) {
+            return static_cast<float>(static_cast<const _Float16*>(p)[idx]);
+        } else {
+            return static_cast<const float*>(p)[idx];
+        }
+    };
+
+    float q[4], o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t d = ln + 64 * j;
+        q[j] = d < hd ? static_cast<float>(to_h(load(a.q, (row_base + i) * a.q_row + h * hd + d))) : 0.0f;
+        o[j] = 0.0f;
+    }
+    const uint32_t n_keys = CAUSAL ? a.pos + i + 1 : a.kv_len;
+    float m_run = -INFINITY, l_run = 0.0f;
+    for (uint32_t t = 0; t < n_keys; ++t) {
+        float dot = 0.0f;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d = ln + 64 * j;
+            float kd = 0.0f, vd = 0.0f;
+            if (d < hd) {
+                if constexpr (CAUSAL) {
+                    kd = static_cast<float>(a.k[static_cast<std::size_t>(t) * a.row + g * hd + d]);
+                    vd = static_cast<float>(a.vt[static_cast<std::size_t>(g * hd + d) * a.ctx_stride + t]);
+                } else {
+                    kd = static_cast<float>(to_h(load(a.k_rows, (row_base + t) * a.row + g * hd + d)));
+                    vd = static_cast<float>(to_h(load(a.v_rows, (row_base + t) * a.row + g * hd + d)));
+                }
+            }
+            dot += q[j] * kd;
+            v[j] = vd;
+        }
+#pragma unroll
+        for (int mask = 32; mask >= 1; mask >>= 1) {
+            dot = xor_sum(dot, mask);
+        }
+        const float m_new = fmaxf(m_run, dot);
+        const float alpha = fast_exp2((m_run - m_new) * c);
+        const float p = static_cast<float>(to_h(fast_exp2((dot - m_new) * c)));
+        l_run = l_run * alpha + p;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            o[j] = o[j] * alpha + p * v[j];
+        }
+        m_run = m_new;
+    }
+    float* out = a.out + (row_base + i) * a.q_row + h * hd;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t d = ln + 64 * j;
+        if (d < hd) {
+            out[d] = o[j] / l_run;
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_generic_causal(const flash_args& a, uint32_t q_dtype, hipStream_t stream) {
+    const dim3 grid(a.n, a.n_heads, 1);
+    if (q_dtype == 1) {
+        generic_kernel<true, true><<<grid, 64, 0, stream>>>(a);
+    } else {
+        generic_kernel<true, false><<<grid, 64, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_generic_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream) {
+    const dim3 grid(a.n, a.n_heads, a.batch);
+    if (in_dtype == 1) {
+        generic_kernel<false, true><<<grid, 64, 0, stream>>>(a);
+    } else {
+        generic_kernel<false, false><<<grid, 64, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace syn

@@ -1,0 +1,109 @@
+// kernels.hpp — host-side launch interface of the attention kernels. Each
+// launcher queues its kernels on `stream` and returns hipGetLastError(); the
+// C ABI (capi.hip) validates every shape and offset before calling one.
+#pragma once
+
+#include "device.hpp"
+
+#include <cstddef>
+#include <cstdint>
+
+namespace syn {
+
+// One KV state resolved to device pointers. K: [max_ctx][n_kv][hd];
+// V^T: [n_kv][hd][ctx_stride].
+struct kv_layout {
+    _Float16* k;
+    _Float16* vt;
+    uint32_t max_ctx, n_kv, hd, ctx_stride;
+};
+
+hipError_t launch_kv_append(const kv_layout& c, const void* k_rows, const void* v_rows, uint32_t n, uint32_t pos0,
+                            uint32_t dtype, hipStream_t stream);
+
+// ---- split-KV decode --------------------------------------------------------
+// One query row attending cache rows 0..len-1.
+struct decode_seq {
+    const void* q;        // n_heads * hd, f32 or f16
+    float* out;           // n_heads * hd
+    const _Float16* k;    // K block
+    const _Float16* vt;   // V^T block
+    uint32_t len;         // attended positions
+    uint32_t ctx_stride;  // V^T row length
+    uint32_t block0;      // first split of this sequence in the launch's split numbering
+    uint32_t n_splits;    // ceil(len / chunk)
+};
+
+constexpr uint32_t decode_max_seqs = 32;  // sequences per launch (kernel-argument table)
+constexpr uint32_t decode_positions_per_wave = 32;
+constexpr uint32_t decode_waves = 4;
+constexpr uint32_t decode_chunk_unit = decode_positions_per_wave * decode_waves;  // 128
+
+struct decode_args {
+    decode_seq seq[decode_max_seqs];
+    uint32_t n_seqs;
+    uint32_t n_kv;
+    uint32_t hd;
+    uint32_t group;        // query heads per KV head, <= 16
+    uint32_t row;          // n_kv * hd: K row length in halves
+    uint32_t chunk;        // positions per split, a multiple of decode_chunk_unit
+    uint32_t counter0;     // first merge counter of this launch
+    float scale_log2e;     // scale * log2(e)
+    float* part_o;         // [splits * n_kv][group][hd]
+    float* part_ml;        // [splits * n_kv][group][2]
+    uint32_t* counters;    // merge counters, zero between launches
+};
+
+// Scratch floats one split contributes: (max, sum, output) for each head.
+inline std::size_t decode_split_floats(uint32_t group, uint32_t hd) {
+    return static_cast<std::size_t>(group) * (hd + 2);
+}
+
+// Picks the chunk (positions per split) for a launch whose sequences attend
+// `total_positions` positions across n_kv heads.
+uint32_t decode_choose_chunk(uint64_t total_positions, uint32_t n_kv);
+
+hipError_t launch_decode(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream);
+
+// ---- flash prefill / bidirectional -----------------------------------------
+struct flash_args {
+    const void* q;         // rows [n][q_row], head h at h * hd
+    float* out;            // rows [n][q_row]
+    // causal over a cache:
+    const _Float16* k;     // K block [max_ctx][row]
+    const _Float16* vt;    // V^T block [row][ctx_stride]
+    // bidirectional over rows:
+    const void* k_rows;    // [n][row]
+    const void* v_rows;
+    uint32_t n;            // query rows (per image)
+    uint32_t batch;        // images (bidirectional), 1 for causal
+    uint32_t pos;          // causal: absolute position of query 0
+    uint32_t kv_len;       // keys attended at most (causal: pos + n; bidirectional: n)
+    uint32_t n_heads, n_kv, hd, group;
+    uint32_t q_row;        // n_heads * hd
+    uint32_t row;          // n_kv * hd
+    uint32_t ctx_stride;
+    float scale_log2e;
+};
+
+hipError_t launch_prefill(const flash_args& a, uint32_t q_dtype, hipStream_t stream);
+hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream);
+
+// ---- any-shape fallback -----------------------------------------------------
+// A plain f32 kernel for shapes the matrix-core kernels do not take
+// (head_dim not a multiple of 8, more than 16 query heads per KV head):
+// causal over a cache, one query row per (token, head).
+hipError_t launch_generic_causal(const flash_args& a, uint32_t q_dtype, hipStream_t stream);
+hipError_t launch_generic_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream);
+
+// ---- RoPE -------------------------------------------------------------------
+struct rope_args {
+    const float* in;
+    float* out;
+    const float* freq_factors;  // or nullptr
+    uint32_t n, size, hd, pos, mode;
+    float theta_scale, freq_scale, ext_factor, attn_factor, corr_low, corr_high;
+};
+hipError_t launch_rope(const rope_args& a, hipStream_t stream);
+
+}  // namespace syn

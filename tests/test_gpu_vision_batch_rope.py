@@ -1,0 +1,162 @@
+"""GPU parity: bidirectional (ViT) self-attention, ragged batched decode,
+RoPE, and the C ABI's descriptor checks."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import binding as orc
+from gpu_util import SYN_F16, SYN_F32, Arena, SeqDesc, capi, check, lib, put_rows, self_attention, seq_array
+from helpers import assert_close
+from synapse_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def arena():
+    a = Arena(3 << 30)
+    yield a
+    a.close()
+
+
+# ---- bidirectional ----------------------------------------------------------
+
+def _vision(arena, n, batch, n_heads, hd, dtype, sigma=0.5, seed=3, images=None):
+    g = wl.rng(seed)
+    shape = (batch * n, n_heads * hd)
+    q, k, v = (wl.normal(g, shape, sigma) for _ in range(3))
+    if dtype == SYN_F16:
+        q, k, v = (x.astype(np.float16).astype(np.float32) for x in (q, k, v))
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    got = self_attention(arena, q, k, v, n, batch, n_heads, scale, dtype)
+    for b in (range(batch) if images is None else images):
+        sl = slice(b * n, (b + 1) * n)
+        want = orc.self_attention(q[sl], k[sl], v[sl], n_heads, scale, threads=8)
+        assert_close(got[sl], want, what=f"image {b} n={n} heads={n_heads} hd={hd}")
+
+
+def test_vision_clip_vit_l14(arena):
+    """Config 5 at full size: 32 images x 257 rows, 16 heads of 64, f16
+    inputs ~ N(0, 0.5^2); four images checked against the oracle."""
+    c = wl.C5
+    _vision(arena, c.n, c.batch, c.n_heads, c.head_dim, SYN_F16, c.sigma, seed=wl.SEED, images=[0, 7, 20, 31])
+
+
+@pytest.mark.parametrize("n,hd", [(37, 8), (1, 8), (6, 16), (50, 24), (130, 64), (257, 128), (64, 256)])
+def test_vision_shapes_f32_inputs(arena, n, hd):
+    """The reference's self-attention cases (tests/sdk/kernels_vision.cpp:
+    200-250, n in {37, 1, 6, 13, 50}) with f32 inputs, which the kernel
+    rounds to binary16 for the matrix cores."""
+    _vision(arena, n, 2, 3, hd, SYN_F32)
+
+
+@pytest.mark.parametrize("n,hd", [(13, 12), (50, 20), (6, 4)])
+def test_vision_generic_head_dims(arena, n, hd):
+    _vision(arena, n, 1, 3, hd, SYN_F32)
+
+
+# ---- ragged batched decode ---------------------------------------------------
+
+def _ragged(arena, lengths, n_heads, n_kv, hd, seed):
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    g = wl.rng(seed)
+    row = n_kv * hd
+    mark = arena.top
+    seqs, refs = [], []
+    for L in lengths:
+        kc = wl.to_f16_bits(wl.rope_rows(wl.normal(g, (L, row)), hd, 0, 500000.0))
+        vc = wl.to_f16_bits(wl.normal(g, (L, row)))
+        q = wl.normal(g, (1, n_heads * hd))
+        cache = capi.kv_state(arena, L, n_kv, hd)
+        capi.upload_cache(arena, cache, kc, vc)
+        q_off = put_rows(arena, q, SYN_F32)
+        out_off = arena.alloc(n_heads * hd * 4)
+        seqs.append(SeqDesc(cache=cache, q_offset=q_off, out_offset=out_off, pos=L - 1))
+        ok_k, ok_v = kc, vc
+        refs.append(orc.attend_rows(q, L - 1, ok_k, ok_v, n_heads, scale, threads=8))
+    arr = seq_array(seqs)
+    need = int(lib().syn_hip_attend_batch_scratch_bytes(arr, len(seqs), n_heads))
+    scratch = arena.alloc(max(need, 256))
+    check(lib().syn_hip_attend_batch(arena.handle, arr, len(seqs), n_heads, scale, SYN_F32, scratch, need))
+    for i, s in enumerate(seqs):
+        got = arena.download(s.out_offset, (1, n_heads * hd), np.float32)
+        assert_close(got, refs[i], what=f"sequence {i} (length {lengths[i]})")
+    arena.top = mark
+
+
+def test_ragged_decode_config4(arena):
+    """Config 4 at full size: 16 sequences, lengths U[512, 32768] from the seed."""
+    c = wl.C4
+    _ragged(arena, [int(x) for x in c.lengths()], c.n_heads, c.n_kv, c.head_dim, seed=wl.SEED)
+
+
+def test_ragged_decode_many_short(arena):
+    """More sequences than one launch takes (32), lengths from 1 up."""
+    lengths = [1, 2, 31, 32, 33, 128, 129, 500] * 5
+    _ragged(arena, lengths, 8, 2, 64, seed=4)
+
+
+# ---- RoPE ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("mode,yarn,ff", [(0, False, False), (1, False, False), (0, True, False), (0, False, True)])
+def test_rope_matches_oracle(arena, mode, yarn, ff):
+    hd, heads, n, pos = 128, 4, 9, 4090
+    g = wl.rng(17)
+    x = wl.normal(g, (n, heads * hd))
+    ts = orc.rope_theta_scale(500000.0, hd)
+    factors = (1.0 + np.arange(hd // 2) % 4).astype(np.float32) if ff else None
+    scaling = [0.25, 1.0, 0.9, 8.0, 23.0] if yarn else None
+    mark = arena.top
+    in_off = put_rows(arena, x, SYN_F32)
+    out_off = arena.alloc(x.nbytes)
+    ff_off = put_rows(arena, factors, SYN_F32) if ff else capi.NO_OFFSET
+    sc = scaling or [1.0, 0.0, 1.0, 0.0, 0.0]
+    d = capi.RopeDesc(in_offset=in_off, out_offset=out_off, freq_factors_offset=ff_off, n=n, size=x.shape[1],
+                      head_dim=hd, pos=pos, theta_scale=ts, mode=mode, freq_scale=sc[0], ext_factor=sc[1],
+                      attn_factor=sc[2], corr_low=sc[3], corr_high=sc[4])
+    check(lib().syn_hip_rope(arena.handle, ctypes.byref(d)))
+    got = arena.download(out_off, x.shape, np.float32)
+    arena.top = mark
+    want = orc.rope_rows(x, hd, pos, ts, freq_factors=factors, mode=mode, scaling=scaling)
+    # Same angles bit for bit (repeated f32 multiplication); cos/sin from two
+    # libraries, each within an ulp or two.
+    assert np.max(np.abs(got - want)) <= 2e-6 * (1 + np.abs(x).max())
+
+
+def test_rope_position_zero_is_identity(arena):
+    x = wl.normal(wl.rng(2), (1, 256))
+    in_off = put_rows(arena, x, SYN_F32)
+    out_off = arena.alloc(x.nbytes)
+    d = capi.RopeDesc(in_offset=in_off, out_offset=out_off, freq_factors_offset=capi.NO_OFFSET, n=1, size=256,
+                      head_dim=64, pos=0, theta_scale=orc.rope_theta_scale(1e4, 64), mode=0, freq_scale=1.0,
+                      ext_factor=0.0, attn_factor=1.0, corr_low=0.0, corr_high=0.0)
+    check(lib().syn_hip_rope(arena.handle, ctypes.byref(d)))
+    assert np.array_equal(arena.download(out_off, x.shape, np.float32), x)
+
+
+# ---- descriptor checks (nothing is launched) ------------------------------------
+
+def test_bad_descriptors_are_errors_not_faults(arena):
+    cache = capi.kv_state(arena, 64, 2, 16)
+    base = dict(cache=cache, q_offset=0, k_offset=0, v_offset=0, out_offset=0, scratch_offset=0, scratch_bytes=0,
+                n_heads=4, pos=0, n=1, scale=0.25, q_dtype=SYN_F32, kv_dtype=SYN_F32)
+
+    def status(**kw):
+        d = capi.AttnDesc(**{**base, **kw})
+        return lib().syn_hip_attention(arena.handle, ctypes.byref(d))
+
+    assert status(q_offset=arena.nbytes - 8) == -2       # q outside the arena
+    assert status(scale=0.0) == -1                       # bad_parameter
+    assert status(scale=float("nan")) == -1
+    assert status(n_heads=3) == -1                       # 3 heads on 2 KV heads
+    assert status(pos=64) == -1                          # past max_ctx
+    assert status(n=0) == -1
+    assert status(q_offset=4) == -1                      # misaligned
+    bad = capi.KvDesc(k_offset=arena.nbytes, v_offset=0, max_ctx=64, n_kv_heads=2, head_dim=16, ctx_stride=64)
+    assert status(cache=bad) == -2
+    bad = capi.KvDesc(k_offset=0, v_offset=0, max_ctx=64, n_kv_heads=2, head_dim=258, ctx_stride=64)
+    assert status(cache=bad) == -1                       # head_dim > 256
+    assert lib().syn_hip_last_error()

@@ -56,8 +56,8 @@ const char* syn_hip_last_error(void);
 
 /* ---- arena (session construction / destruction) ------------------------
  * Replaces session's arena + states allocation (S/graph/session.hpp:90-95,
- * :193-197) with one device allocation of `bytes` bytes, 256-B aligned, on
- * the current HIP device, plus the library's own control words (zeroed). */
+ * :193-197) with one device allocation of `bytes` (> 0) bytes, 256-B
+ * aligned, on the current HIP device, and one HIP stream. */
 int syn_hip_arena_create(size_t bytes, syn_arena** out);
 int syn_hip_arena_destroy(syn_arena* arena);
 size_t syn_hip_arena_bytes(const syn_arena* arena);

@@ -16,17 +16,14 @@
 #include <string>
 
 struct syn_arena {
-    char* base = nullptr;          // user bytes, then the control block
-    std::size_t bytes = 0;         // user bytes
-    uint32_t* counters = nullptr;  // decode merge counters (control block)
+    char* base = nullptr;   // device bytes
+    std::size_t bytes = 0;  // usable bytes (the allocation is rounded up to 256)
     hipStream_t stream = nullptr;
     int device = 0;
 };
 
 namespace {
 
-constexpr uint32_t n_counters = 16384;
-constexpr std::size_t control_bytes = n_counters * sizeof(uint32_t);
 constexpr uint64_t no_offset = ~uint64_t{0};
 
 thread_local char last_error[512] = "";
@@ -128,21 +125,35 @@ uint64_t decode_scratch_bytes(uint32_t splits, uint32_t n_kv, uint32_t group, ui
 }
 
 // One decode launch over seqs[0..n): fills the argument block, checks the
-// scratch, launches.
+// scratch, launches. kv_dtype types the sequences' k_new / v_new rows.
 int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n_kv, uint32_t hd, uint32_t group,
-               float scale, uint32_t q_dtype, uint64_t scratch_offset, uint64_t scratch_bytes) {
+               float scale, uint32_t q_dtype, uint32_t kv_dtype, uint64_t scratch_offset, uint64_t scratch_bytes) {
     syn::decode_args args{};
     uint64_t positions = 0;
+    uint32_t max_len = 0;
     for (uint32_t i = 0; i < n; ++i) {
         positions += seqs[i].len;
+        max_len = std::max(max_len, seqs[i].len);
     }
-    const uint32_t chunk = syn::decode_choose_chunk(positions, n_kv);
+    const uint32_t chunk = syn::decode_choose_chunk(positions, n_kv, max_len);
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!syn::decode_fits(chunk, n_kv * hd, hd, seqs[i].ctx_stride)) {
+            return fail(SYN_HIP_EUNSUPPORTED, "decode: a split or V^T row span exceeds 2^31 bytes");
+        }
+    }
     uint32_t splits = 0;
+    uint32_t merge_blocks = 0;
     for (uint32_t i = 0; i < n; ++i) {
         args.seq[i] = seqs[i];
         args.seq[i].block0 = splits;
         args.seq[i].n_splits = (seqs[i].len + chunk - 1) / chunk;
+        args.seq[i].merge0 = merge_blocks;
+        args.block0s[i] = splits;
+        args.merge0s[i] = merge_blocks;
         splits += args.seq[i].n_splits;
+        if (args.seq[i].n_splits > 1) {
+            merge_blocks += n_kv * group;
+        }
     }
     args.n_seqs = n;
     args.n_kv = n_kv;
@@ -150,14 +161,10 @@ int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n
     args.group = group;
     args.row = n_kv * hd;
     args.chunk = chunk;
-    args.counter0 = 0;
+    args.kv_dtype = kv_dtype;
+    args.merge_blocks = merge_blocks;
     args.scale_log2e = scale * syn::log2e;
-    args.counters = a->counters;
-    bool any_split = false;
-    for (uint32_t i = 0; i < n; ++i) {
-        any_split = any_split || args.seq[i].n_splits > 1;
-    }
-    if (any_split) {
+    if (merge_blocks > 0) {
         const uint64_t need = decode_scratch_bytes(splits, n_kv, group, hd);
         if (need > scratch_bytes) {
             return fail(SYN_HIP_EINVAL, "decode: scratch of %llu bytes, %llu needed",
@@ -169,10 +176,6 @@ int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n
         float* part = reinterpret_cast<float*>(a->base + scratch_offset);
         args.part_o = part;
         args.part_ml = part + uint64_t{splits} * n_kv * group * hd;
-    }
-    if (uint64_t{n} * n_kv > n_counters) {
-        return fail(SYN_HIP_EUNSUPPORTED, "decode: %u sequences x %u KV heads exceed %u merge counters", n, n_kv,
-                    n_counters);
     }
     return hip_status(syn::launch_decode(args, splits, q_dtype, a->stream), "decode launch");
 }
@@ -241,19 +244,33 @@ syn::flash_args flash_of(syn_arena* a, const syn_attn_desc* d) {
     return f;
 }
 
-int attend_checked(syn_arena* a, const syn_attn_desc* d) {
+bool decode_shape(const syn_attn_desc* d) {
+    const syn_kv_desc& c = d->cache;
+    const uint32_t len = d->pos + 1;
+    return d->n == 1 && fast_shape(c.head_dim) && d->n_heads / c.n_kv_heads <= 16 &&
+           syn::decode_fits(syn::decode_choose_chunk(len, c.n_kv_heads, len), c.n_kv_heads * c.head_dim, c.head_dim,
+                            c.ctx_stride);
+}
+
+// Attends the run; with_new_rows, a single-token step's K, V row is appended
+// by the decode kernel itself (one launch), longer runs were appended before.
+int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows) {
     const syn_kv_desc& c = d->cache;
     const uint32_t group = d->n_heads / c.n_kv_heads;
-    if (d->n == 1 && fast_shape(c.head_dim) && group <= 16) {
+    if (decode_shape(d)) {
         syn::decode_seq s{};
         s.q = a->base + d->q_offset;
         s.out = reinterpret_cast<float*>(a->base + d->out_offset);
-        s.k = reinterpret_cast<const _Float16*>(a->base + c.k_offset);
-        s.vt = reinterpret_cast<const _Float16*>(a->base + c.v_offset);
+        s.k = reinterpret_cast<_Float16*>(a->base + c.k_offset);
+        s.vt = reinterpret_cast<_Float16*>(a->base + c.v_offset);
+        if (with_new_rows) {
+            s.k_new = a->base + d->k_offset;
+            s.v_new = a->base + d->v_offset;
+        }
         s.len = d->pos + 1;
         s.ctx_stride = c.ctx_stride;
-        return run_decode(a, &s, 1, c.n_kv_heads, c.head_dim, group, d->scale, d->q_dtype, d->scratch_offset,
-                          d->scratch_bytes);
+        return run_decode(a, &s, 1, c.n_kv_heads, c.head_dim, group, d->scale, d->q_dtype, d->kv_dtype,
+                          d->scratch_offset, d->scratch_bytes);
     }
     const syn::flash_args f = flash_of(a, d);
     if (fast_shape(c.head_dim)) {
@@ -306,7 +323,7 @@ int syn_hip_arena_create(size_t bytes, syn_arena** out) {
         return fail(SYN_HIP_ENODEV, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
     }
     const std::size_t user = align256(bytes);
-    if (user < bytes || user > SIZE_MAX - control_bytes) {
+    if (bytes == 0 || user < bytes) {
         return fail(SYN_HIP_EINVAL, "arena of %zu bytes", bytes);
     }
     auto* a = new (std::nothrow) syn_arena;
@@ -314,30 +331,17 @@ int syn_hip_arena_create(size_t bytes, syn_arena** out) {
         return fail(SYN_HIP_ENOMEM, "host allocation failed");
     }
     void* p = nullptr;
-    if (hipMalloc(&p, user + control_bytes) != hipSuccess) {
+    if (hipMalloc(&p, user) != hipSuccess) {
         delete a;
-        return fail(SYN_HIP_ENOMEM, "hipMalloc of %zu bytes failed", user + control_bytes);
+        return fail(SYN_HIP_ENOMEM, "hipMalloc of %zu bytes failed", user);
     }
     a->base = static_cast<char*>(p);
     a->bytes = bytes;
-    a->counters = reinterpret_cast<uint32_t*>(a->base + user);
     a->device = device;
     if (hipStreamCreateWithFlags(&a->stream, hipStreamNonBlocking) != hipSuccess) {
         (void)hipFree(p);
         delete a;
         return fail(SYN_HIP_ENOMEM, "hipStreamCreate failed");
-    }
-    if (int e = hip_status(hipMemsetAsync(a->counters, 0, control_bytes, a->stream), "control block")) {
-        (void)hipStreamDestroy(a->stream);
-        (void)hipFree(p);
-        delete a;
-        return e;
-    }
-    if (int e = hip_status(hipStreamSynchronize(a->stream), "arena init")) {
-        (void)hipStreamDestroy(a->stream);
-        (void)hipFree(p);
-        delete a;
-        return e;
     }
     *out = a;
     return SYN_HIP_OK;
@@ -490,17 +494,20 @@ int syn_hip_attention(syn_arena* a, const syn_attn_desc* d) {
     if (int e = check_attn(a, d, true)) {
         return e;
     }
+    if (decode_shape(d)) {
+        return attend_checked(a, d, true);  // the decode kernel appends the row itself
+    }
     if (int e = syn_hip_kv_append(a, &d->cache, d->k_offset, d->v_offset, d->n, d->pos, d->kv_dtype)) {
         return e;
     }
-    return attend_checked(a, d);
+    return attend_checked(a, d, false);
 }
 
 int syn_hip_attend(syn_arena* a, const syn_attn_desc* d) {
     if (int e = check_attn(a, d, false)) {
         return e;
     }
-    return attend_checked(a, d);
+    return attend_checked(a, d, false);
 }
 
 uint64_t syn_hip_attend_batch_scratch_bytes(const syn_seq_desc* seqs, uint32_t n_seqs, uint32_t n_heads) {
@@ -513,10 +520,12 @@ uint64_t syn_hip_attend_batch_scratch_bytes(const syn_seq_desc* seqs, uint32_t n
     for (uint32_t b0 = 0; b0 < n_seqs; b0 += syn::decode_max_seqs) {
         const uint32_t nb = std::min(n_seqs - b0, syn::decode_max_seqs);
         uint64_t positions = 0;
+        uint32_t max_len = 0;
         for (uint32_t i = 0; i < nb; ++i) {
             positions += uint64_t{seqs[b0 + i].pos} + 1;
+            max_len = std::max(max_len, seqs[b0 + i].pos + 1);
         }
-        const uint32_t chunk = syn::decode_choose_chunk(positions, n_kv);
+        const uint32_t chunk = syn::decode_choose_chunk(positions, n_kv, max_len);
         uint64_t splits = 0;
         for (uint32_t i = 0; i < nb; ++i) {
             splits += (uint64_t{seqs[b0 + i].pos} + chunk) / chunk;
@@ -563,7 +572,21 @@ int syn_hip_attend_batch(syn_arena* a, const syn_seq_desc* seqs, uint32_t n_seqs
         return fail(SYN_HIP_EINVAL, "attend_batch: %u query heads on %u KV heads", n_heads, n_kv);
     }
     const uint32_t group = n_heads / n_kv;
-    if (!fast_shape(hd) || group > 16) {
+    bool fits = true;
+    for (uint32_t b0 = 0; b0 < n_seqs; b0 += syn::decode_max_seqs) {
+        const uint32_t nb = std::min(n_seqs - b0, syn::decode_max_seqs);
+        uint64_t positions = 0;
+        uint32_t max_len = 0;
+        for (uint32_t i = 0; i < nb; ++i) {
+            positions += uint64_t{seqs[b0 + i].pos} + 1;
+            max_len = std::max(max_len, seqs[b0 + i].pos + 1);
+        }
+        const uint32_t chunk = syn::decode_choose_chunk(positions, n_kv, max_len);
+        for (uint32_t i = 0; i < nb; ++i) {
+            fits = fits && syn::decode_fits(chunk, n_kv * hd, hd, seqs[b0 + i].cache.ctx_stride);
+        }
+    }
+    if (!fast_shape(hd) || group > 16 || !fits) {
         // Shapes outside the split-KV kernel: one causal launch per sequence.
         for (uint32_t i = 0; i < n_seqs; ++i) {
             syn_attn_desc d{};
@@ -590,12 +613,12 @@ int syn_hip_attend_batch(syn_arena* a, const syn_seq_desc* seqs, uint32_t n_seqs
             ds[i] = syn::decode_seq{};
             ds[i].q = a->base + s.q_offset;
             ds[i].out = reinterpret_cast<float*>(a->base + s.out_offset);
-            ds[i].k = reinterpret_cast<const _Float16*>(a->base + s.cache.k_offset);
-            ds[i].vt = reinterpret_cast<const _Float16*>(a->base + s.cache.v_offset);
+            ds[i].k = reinterpret_cast<_Float16*>(a->base + s.cache.k_offset);
+            ds[i].vt = reinterpret_cast<_Float16*>(a->base + s.cache.v_offset);
             ds[i].len = s.pos + 1;
             ds[i].ctx_stride = s.cache.ctx_stride;
         }
-        if (int e = run_decode(a, ds, nb, n_kv, hd, group, scale, q_dtype, scratch_offset, scratch_bytes)) {
+        if (int e = run_decode(a, ds, nb, n_kv, hd, group, scale, q_dtype, SYN_F32, scratch_offset, scratch_bytes)) {
             return e;
         }
     }

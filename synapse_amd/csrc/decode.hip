@@ -20,10 +20,21 @@
 // f16 as the reference rounds it (:225-227) -- before normalisation here,
 // which the online form needs.
 //
-// The 4 waves merge their (max, sum, O) through LDS; splits then merge in the
-// same launch: each block publishes its partial, and the last block of a
-// (sequence, KV head) to finish (an agent-scope counter) combines all splits
-// in split order, so the result is deterministic, and resets the counter.
+// The 4 waves merge their (max, sum, O) through LDS. A sequence with more
+// than one split then needs its splits combined: each block writes its
+// unnormalised partial (max, sum, O) to scratch, and a second small kernel on
+// the same stream merges them, one block per (sequence, query head). The
+// kernel boundary is what makes the partials visible: an in-kernel
+// "last block merges" handoff needs an agent-scope release per block, which
+// on this multi-XCD part writes back the whole L2 each time and costs far
+// more than the second launch. The merge stages through LDS: one wave turns
+// the splits' (max, sum) into weights with shuffles, then all threads stream
+// the partial outputs with independent 16-byte loads. Each output sums its
+// splits in a fixed order, so results are deterministic.
+//
+// A single-token step passes its new K, V row (k_new, v_new): the block whose
+// split ends at that position rounds it to binary16, attends it from
+// registers and stores it into the cache, so the step is one launch.
 
 #include "kernels.hpp"
 
@@ -31,33 +42,64 @@ namespace syn {
 
 namespace {
 
-template <int HDP, bool QF16>
-__device__ __forceinline__ h8 load_q8(const void* q, std::size_t index) {
-    if constexpr (QF16) {
-        return as_h8(load16(static_cast<const _Float16*>(q) + index));
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        v = xor_max(v, m);
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        v = xor_sum(v, m);
+    }
+    return v;
+}
+
+// The sequence a block belongs to: starts[] is non-decreasing, and sequence
+// i owns blocks [starts[i], starts[i+1]). All loads are independent, so they
+// go out as one batch; a single-sequence launch needs none.
+template <bool MULTI>
+__device__ __forceinline__ uint32_t find_seq(const uint32_t* starts, uint32_t n, uint32_t x) {
+    if constexpr (!MULTI) {
+        return 0;
     } else {
-        const float* p = static_cast<const float*>(q) + index;
-        const f4 lo = *reinterpret_cast<const f4*>(p);
-        const f4 hi = *reinterpret_cast<const f4*>(p + 4);
-        h8 r;
-        r[0] = to_h(lo[0]);
-        r[1] = to_h(lo[1]);
-        r[2] = to_h(lo[2]);
-        r[3] = to_h(lo[3]);
-        r[4] = to_h(hi[0]);
-        r[5] = to_h(hi[1]);
-        r[6] = to_h(hi[2]);
-        r[7] = to_h(hi[3]);
-        return r;
+        uint32_t si = 0;
+#pragma unroll
+        for (uint32_t i = 1; i < decode_max_seqs; ++i) {
+            si += (i < n && x >= starts[i]) ? 1u : 0u;
+        }
+        return si;
     }
 }
 
-template <int HDP, bool QF16>
+// LDS of the split kernel: the group's q as given (f32 size, the larger),
+// the new K and V row of one head (likewise), per-wave (max, sum), then the
+// waves' unscaled outputs, head rows padded by 4 floats.
+inline __host__ __device__ uint32_t q_lds_bytes(uint32_t group, uint32_t hd) {
+    return (group * hd * 4 + 15) / 16 * 16;
+}
+inline __host__ __device__ uint32_t new_lds_bytes(uint32_t hd) {
+    return (2 * hd * 4 + 15) / 16 * 16;
+}
+inline std::size_t decode_lds_bytes(uint32_t group, uint32_t hd) {
+    return q_lds_bytes(group, hd) + new_lds_bytes(hd) + (4 * 16 * 2 + 4 * std::size_t{group} * (hd + 4)) * sizeof(float);
+}
+
+// s_waitcnt immediate that waits until at most n vector memory operations
+// are outstanding (gfx9 encoding: vmcnt split over bits 3:0 and 15:14;
+// expcnt and lgkmcnt left at their no-wait maxima).
+constexpr int vmcnt_imm(int n) {
+    return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
+template <int HDP, bool QF16, bool MULTI>
 __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     constexpr int NS = HDP / 32;   // k-steps of the score product
     constexpr int NT = HDP / 16;   // 16-dim tiles of the output
     constexpr int SPAN = HDP / 4;  // dims a lane group holds across the k-steps
-    extern __shared__ float lds[];  // [4][16][2] (max, sum), then [2][group][hd]
 
     const int tid = threadIdx.x;
     const int w = tid >> 6;
@@ -72,28 +114,78 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     const uint32_t b = blockIdx.x;
     const uint32_t g = b % a.n_kv;
     const uint32_t sb = b / a.n_kv;
-    uint32_t si = 0;
-    while (si + 1 < a.n_seqs && sb >= a.seq[si + 1].block0) {
-        ++si;
-    }
-    const decode_seq s = a.seq[si];
+    const uint32_t si = find_seq<MULTI>(a.block0s, a.n_seqs, sb);
+    const decode_seq& s = a.seq[si];
     const uint32_t split = sb - s.block0;
     const uint32_t t_begin = split * a.chunk;
     const uint32_t t_end = min(s.len, t_begin + a.chunk);
     const uint32_t h0 = g * group;
     const float c = a.scale_log2e;
+    // The step's new row (position len-1) is in this block's split: take it
+    // from k_new / v_new, rounded to binary16, and store it into the cache.
+    const uint32_t new_t = s.len - 1;
+    const bool new_here = s.k_new != nullptr && t_end == s.len;
+    const bool kv_f16 = a.kv_dtype == 1;
 
-    // q^T operand: lane (G, r) holds head h0 + r, dims G*SPAN + 8*st + [0, 8).
-    h8 qv[NS];
-#pragma unroll
-    for (int st = 0; st < NS; ++st) {
-        const uint32_t d0 = G * SPAN + 8 * st;
-        if (static_cast<uint32_t>(r) < group && d0 < hd) {
-            qv[st] = load_q8<HDP, QF16>(s.q, static_cast<std::size_t>(h0 + r) * hd + d0);
-        } else {
-            qv[st] = as_h8(zero_u4());
+    // Every K, V load below is unconditional, so a wave issues all of them
+    // back to back: a lane with nothing to read points at valid data and
+    // zeroes what it got afterwards.
+    //
+    // The group's q rows are copied once per block into LDS, 1 KB per wave
+    // instruction, straight from global memory (no registers): every wave of
+    // every split reading q itself would pile thousands of requests onto the
+    // same few lines.
+    extern __shared__ __attribute__((aligned(16))) char lds_bytes[];
+    const uint32_t q_bytes = group * hd * (QF16 ? 2 : 4);
+    const char* q_src = static_cast<const char*>(s.q) + static_cast<std::size_t>(h0) * hd * (QF16 ? 2 : 4);
+    for (uint32_t c0 = 1024 * w; c0 < q_bytes; c0 += 4096) {
+        // q_bytes is a multiple of 16; a lane past its end re-reads chunk 0.
+        const uint32_t off = c0 + 16 * ln < q_bytes ? c0 + 16 * ln : 0;
+        load16_lds(q_src + off, lds_bytes + c0);
+    }
+    // The block holding the step's new row stages that row of KV head g the
+    // same way (K then V, as given), for the step that appends it.
+    char* new_lds = lds_bytes + q_lds_bytes(group, hd);
+    const uint32_t new_bytes = hd * (kv_f16 ? 2 : 4);
+    if (new_here) {
+        const std::size_t row_off = static_cast<std::size_t>(g) * new_bytes;
+        for (uint32_t c0 = 1024 * w; c0 < 2 * new_bytes; c0 += 4096) {
+            const uint32_t c = c0 + 16 * ln < 2 * new_bytes ? c0 + 16 * ln : 0;
+            const char* src = c < new_bytes ? static_cast<const char*>(s.k_new) + row_off + c
+                                            : static_cast<const char*>(s.v_new) + row_off + (c - new_bytes);
+            load16_lds(src, new_lds + c0);
         }
     }
+
+    // K rows for the two S^T tiles: row r of tile e is position
+    // tb + 8*(r/4) + 4*e + r%4, so accumulator row 4G+i of tile e is position
+    // tb + 8G + 4e + i. V^T rows: lane (G, r) of tile n holds dim 16n + r at
+    // positions tb + 8G + [0, 8). Both through buffer resources based at the
+    // split: K past the split and dims past the head read as zeros.
+    _Float16* kbase = s.k + g * hd + G * SPAN;
+    const uint32_t row2 = a.row * 2;
+    const uint32_t vstride2 = s.ctx_stride * 2;
+    const rsrc k_res = make_rsrc(s.k + static_cast<std::size_t>(t_begin) * a.row + g * hd,
+                                 (t_end - t_begin) * row2 - g * hd * 2);
+    const rsrc v_res = make_rsrc(s.vt + static_cast<std::size_t>(g) * hd * s.ctx_stride + t_begin,
+                                 hd * vstride2 - t_begin * 2);
+    const auto load_kv = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t rel = tb - t_begin + 8 * (r >> 2) + 4 * e + (r & 3);
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                const uint32_t d0 = G * SPAN + 8 * st;
+                kr[e][st] = buffer_load16(k_res, d0 < hd ? rel * row2 + d0 * 2 : buffer_oob);
+            }
+        }
+        const uint32_t rel_v = (tb - t_begin + 8 * G) * 2;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const uint32_t dim = 16 * n + r;
+            vr[n] = buffer_load16(v_res, dim < hd ? dim * vstride2 + rel_v : buffer_oob);
+        }
+    };
 
     float m_run = -INFINITY;  // running max of raw q.k for head r
     float l_run = 0.0f;       // running sum of f16-rounded p for head r
@@ -102,32 +194,81 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     for (int n = 0; n < NT; ++n) {
         o[n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-
-    const _Float16* kbase = s.k + g * hd + G * SPAN;
-    for (uint32_t tb = t_begin + decode_positions_per_wave * w; tb < t_end;
-         tb += decode_positions_per_wave * decode_waves) {
-        // K rows for the two S^T tiles: row r of tile e is position
-        // tb + 8*(r/4) + 4*e + r%4, so accumulator row 4G+i of tile e is
-        // position tb + 8G + 4e + i.
-        u4 kr[2][NS];
+    // q^T operand: lane (G, r) holds head h0 + r, dims G*SPAN + 8*st + [0, 8),
+    // rounded to binary16 as attend_group rounds q (S/kernels/attention.hpp:204-206).
+    h8 qv[NS];
+    const auto convert_q = [&]() {
+        // Wait for q's copy only: the K, V loads issued after it stay in flight.
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NS + NT));
+        __syncthreads();
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const uint32_t t = tb + 8 * (r >> 2) + 4 * e + (r & 3);
-            const _Float16* kp = kbase + static_cast<std::size_t>(t) * a.row;
-#pragma unroll
-            for (int st = 0; st < NS; ++st) {
-                const bool ok = t < s.len && G * SPAN + 8 * st < hd;
-                kr[e][st] = ok ? load16(kp + 8 * st) : zero_u4();
+        for (int st = 0; st < NS; ++st) {
+            const uint32_t d0 = G * SPAN + 8 * st;
+            const uint32_t e0 = static_cast<uint32_t>(r) * hd + d0;
+            if (static_cast<uint32_t>(r) < group && d0 < hd) {
+                if constexpr (QF16) {
+                    qv[st] = *reinterpret_cast<const h8*>(lds_bytes + 2 * e0);
+                } else {
+                    const f4 lo = *reinterpret_cast<const f4*>(lds_bytes + 4 * e0);
+                    const f4 hi = *reinterpret_cast<const f4*>(lds_bytes + 4 * e0 + 16);
+                    qv[st] = h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]),
+                                to_h(hi[0]), to_h(hi[1]), to_h(hi[2]), to_h(hi[3])};
+                }
+            } else {
+                qv[st] = as_h8(zero_u4());
             }
         }
-        // V^T rows: lane (G, r) of tile n holds dim 16n + r at positions tb + 8G + [0, 8).
+    };
+
+    // One 32-position step of the wave on loaded K, V.
+    const auto step = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
         const uint32_t tv = tb + 8 * G;
-        u4 vr[NT];
+        if (new_here && tb + decode_positions_per_wave > new_t) {
+            // kv_append (S/kernels/attention.hpp:165-175) of the new row, from
+            // its LDS copy: into this step's operands and into the cache.
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            const uint32_t dim = 16 * n + r;
-            const bool ok = dim < hd && tv < s.len;
-            vr[n] = ok ? load16(s.vt + static_cast<std::size_t>(g * hd + dim) * s.ctx_stride + tv) : zero_u4();
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t t = tb + 8 * (r >> 2) + 4 * e + (r & 3);
+                if (t == new_t) {
+                    _Float16* kp = kbase + static_cast<std::size_t>(t) * a.row;
+#pragma unroll
+                    for (int st = 0; st < NS; ++st) {
+                        const uint32_t d0 = G * SPAN + 8 * st;
+                        if (d0 < hd) {
+                            if (kv_f16) {
+                                kr[e][st] = *reinterpret_cast<const u4*>(new_lds + 2 * d0);
+                            } else {
+                                const f4 lo = *reinterpret_cast<const f4*>(new_lds + 4 * d0);
+                                const f4 hi = *reinterpret_cast<const f4*>(new_lds + 4 * d0 + 16);
+                                kr[e][st] = as_u4(h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]),
+                                                     to_h(hi[0]), to_h(hi[1]), to_h(hi[2]), to_h(hi[3])});
+                            }
+                            store16(kp + 8 * st, kr[e][st]);
+                        }
+                    }
+                }
+            }
+            if (tv <= new_t && new_t < tv + 8) {
+                const uint32_t j = new_t - tv;
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const uint32_t dim = 16 * n + r;
+                    if (dim < hd) {
+                        const _Float16 x =
+                            kv_f16 ? *reinterpret_cast<const _Float16*>(new_lds + new_bytes + 2 * dim)
+                                   : to_h(*reinterpret_cast<const float*>(new_lds + new_bytes + 4 * dim));
+                        h8 v = as_h8(vr[n]);
+#pragma unroll
+                        for (uint32_t jj = 0; jj < 8; ++jj) {
+                            if (jj == j) {
+                                v[jj] = x;
+                            }
+                        }
+                        vr[n] = as_u4(v);
+                        s.vt[static_cast<std::size_t>(g * hd + dim) * s.ctx_stride + new_t] = x;
+                    }
+                }
+            }
         }
 
         f4 sc[2];
@@ -150,8 +291,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
                 bm = fmaxf(bm, sc[e][i]);
             }
         }
-        bm = xor_max(bm, 16);
-        bm = xor_max(bm, 32);
+        bm = max32(max16(bm));
         const float m_new = fmaxf(m_run, bm);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         const float alpha = fast_exp2((m_run - m_use) * c);
@@ -166,19 +306,12 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
                 ps += static_cast<float>(ph);
             }
         }
-        ps = xor_sum(ps, 16);
-        ps = xor_sum(ps, 32);
-        l_run = l_run * alpha + ps;
+        l_run = l_run * alpha + sum32(sum16(ps));
         m_run = m_new;
-
-        // Output rows are heads 4G + i: fetch their rescale factors.
+        // The O^T accumulator's column is this lane's head: rescale by its own alpha.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float ai = __shfl(alpha, 4 * G + i, wave);
-#pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                o[n][i] *= ai;
-            }
+        for (int n = 0; n < NT; ++n) {
+            o[n] *= alpha;
         }
         // Positions past the split end carry p = 0; zero their V too, so a
         // stale non-finite half past the cache's length cannot reach O.
@@ -195,151 +328,226 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
                 vr[n] = as_u4(v);
             }
         }
+        // O^T (16 dims x 16 heads) += V^T (16 dims x 32 positions) . P^T: the
+        // V^T rows and the score registers are the operands as they stand.
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-            o[n] = mfma16(pa, as_h8(vr[n]), o[n]);
+            o[n] = mfma16(as_h8(vr[n]), pa, o[n]);
+        }
+    };
+
+    // The wave's first K, V loads go out with q's; later steps load their
+    // 32 positions at the top of the step.
+    constexpr uint32_t stride = decode_positions_per_wave * decode_waves;
+    u4 kr[2][NS], vr[NT];
+    uint32_t tb = t_begin + decode_positions_per_wave * w;
+    if (tb < t_end) {
+        load_kv(tb, kr, vr);
+    }
+    convert_q();
+    while (tb < t_end) {
+        step(tb, kr, vr);
+        tb += stride;
+        if (tb < t_end) {
+            load_kv(tb, kr, vr);
         }
     }
 
-    // ---- merge the 4 waves ---------------------------------------------------
-    float* lds_ml = lds;
-    float* lds_o = lds + 4 * 16 * 2;
+    // ---- merge the 4 waves (one barrier) -----------------------------------------
+    // Each wave leaves its per-head (max, sum) and its unscaled O^T in its own
+    // LDS slot (head rows padded by 4 floats against bank conflicts); then
+    // every thread combines the 4 slots for its output elements. Lane (G, r)
+    // holds O^T[16n + 4G + i][head r] in o[n][i].
+    const uint32_t orow = hd + 4;
+    float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));
+    float* lds_o = lds_ml + 4 * 16 * 2;
     if (G == 0) {
         lds_ml[(w * 16 + r) * 2] = m_run;
         lds_ml[(w * 16 + r) * 2 + 1] = l_run;
     }
-    __syncthreads();
-    float fac[4];
+    if (static_cast<uint32_t>(r) < group) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int h = 4 * G + i;
-        float mx = lds_ml[h * 2];
-#pragma unroll
-        for (int v = 1; v < 4; ++v) {
-            mx = fmaxf(mx, lds_ml[(v * 16 + h) * 2]);
-        }
-        fac[i] = fast_exp2((lds_ml[(w * 16 + h) * 2] - mx) * c);
-    }
-    // Waves 0, 1 store their scaled O; waves 2, 3 then add theirs on top.
-    const int slot = w & 1;
-    for (int phase = 0; phase < 2; ++phase) {
-        if ((w >> 1) == phase) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t h = 4 * G + i;
-                if (h < group) {
-#pragma unroll
-                    for (int n = 0; n < NT; ++n) {
-                        const uint32_t d = 16 * n + r;
-                        if (d < hd) {
-                            float* dst = lds_o + (slot * group + h) * hd + d;
-                            const float v = o[n][i] * fac[i];
-                            *dst = phase == 0 ? v : *dst + v;
-                        }
-                    }
-                }
+        for (int n = 0; n < NT; ++n) {
+            const uint32_t d0 = 16 * n + 4 * G;
+            if (d0 < hd) {
+                *reinterpret_cast<f4*>(lds_o + (w * group + r) * orow + d0) = o[n];
             }
         }
-        __syncthreads();
     }
+    __syncthreads();
 
     const uint32_t nout = group * hd;
-    if (s.n_splits == 1) {
-        float* out = s.out + static_cast<std::size_t>(h0) * hd;
-        for (uint32_t e = tid; e < nout; e += 256) {
-            const uint32_t h = e / hd;
-            float mx = lds_ml[h * 2];
-            for (int v = 1; v < 4; ++v) {
-                mx = fmaxf(mx, lds_ml[(v * 16 + h) * 2]);
-            }
-            float sum = 0.0f;
-            for (int v = 0; v < 4; ++v) {
-                sum += lds_ml[(v * 16 + h) * 2 + 1] * fast_exp2((lds_ml[(v * 16 + h) * 2] - mx) * c);
-            }
-            out[e] = (lds_o[e] + lds_o[nout + e]) / sum;
-        }
-        return;
-    }
-
-    // ---- publish this split's partial ------------------------------------------
     for (uint32_t e = tid; e < nout; e += 256) {
         const uint32_t h = e / hd;
         const uint32_t d = e % hd;
-        a.part_o[static_cast<std::size_t>(b) * nout + e] = lds_o[e] + lds_o[nout + e];
-        if (d == 0) {
-            float mx = lds_ml[h * 2];
-            for (int v = 1; v < 4; ++v) {
-                mx = fmaxf(mx, lds_ml[(v * 16 + h) * 2]);
-            }
-            float sum = 0.0f;
-            for (int v = 0; v < 4; ++v) {
-                sum += lds_ml[(v * 16 + h) * 2 + 1] * fast_exp2((lds_ml[(v * 16 + h) * 2] - mx) * c);
-            }
-            a.part_ml[(static_cast<std::size_t>(b) * group + h) * 2] = mx;
-            a.part_ml[(static_cast<std::size_t>(b) * group + h) * 2 + 1] = sum;
+        float mw[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            mw[v] = lds_ml[(v * 16 + h) * 2];
+            mx = fmaxf(mx, mw[v]);
         }
-    }
-    __threadfence();  // this thread's partial stores, visible device-wide
-    __syncthreads();
-    __shared__ uint32_t last;
-    uint32_t* counter = a.counters + a.counter0 + si * a.n_kv + g;
-    if (tid == 0) {
-        last = atomicAdd(counter, 1u) == s.n_splits - 1 ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!last) {
-        return;
-    }
-    __threadfence();  // acquire every other split's partial
-
-    // ---- last block: combine the splits in split order -------------------------
-    float* out = s.out + static_cast<std::size_t>(h0) * hd;
-    for (uint32_t e = tid; e < nout; e += 256) {
-        const uint32_t h = e / hd;
-        float mx = -INFINITY, sum = 0.0f, acc = 0.0f;
-        for (uint32_t j = 0; j < s.n_splits; ++j) {
-            const std::size_t pb = static_cast<std::size_t>(s.block0 + j) * a.n_kv + g;
-            const float mj = a.part_ml[(pb * group + h) * 2];
-            const float lj = a.part_ml[(pb * group + h) * 2 + 1];
-            const float oj = a.part_o[pb * nout + e];
-            const float m_new = fmaxf(mx, mj);
-            const float sa = fast_exp2((mx - m_new) * c);
-            const float sj = fast_exp2((mj - m_new) * c);
-            sum = sum * sa + lj * sj;
-            acc = acc * sa + oj * sj;
-            mx = m_new;
+        float sum = 0.0f, acc = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float f = fast_exp2((mw[v] - mx) * c);  // 0 for a wave with no positions
+            sum += lds_ml[(v * 16 + h) * 2 + 1] * f;
+            acc += lds_o[(v * group + h) * orow + d] * f;
         }
-        out[e] = acc / sum;
-    }
-    if (tid == 0) {
-        *counter = 0u;  // ready for the next launch
+        if (s.n_splits == 1) {
+            s.out[static_cast<std::size_t>(h0) * hd + e] = acc / sum;
+        } else {
+            // This split's partial; the merge kernel combines them.
+            a.part_o[static_cast<std::size_t>(b) * nout + e] = acc;
+            if (d == 0) {
+                a.part_ml[(static_cast<std::size_t>(b) * group + h) * 2] = mx;
+                a.part_ml[(static_cast<std::size_t>(b) * group + h) * 2 + 1] = sum;
+            }
+        }
     }
 }
 
-template <int HDP>
+// One block per (sequence with splits, query head): out = sum_j w_j O_j with
+// w_j = exp2((m_j - max) c) / sum_i l_i exp2((m_i - max) c).
+template <bool MULTI>
+__global__ __launch_bounds__(256) void decode_merge_kernel(const decode_args a) {
+    __shared__ float wts[decode_max_splits];
+    __shared__ f4 acc_lds[256];
+    const int tid = threadIdx.x;
+    const int ln = tid & 63;
+    const uint32_t u = blockIdx.x;
+    const uint32_t si = find_seq<MULTI>(a.merge0s, a.n_seqs, u);
+    const decode_seq& s = a.seq[si];
+    const uint32_t k = u - s.merge0;
+    const uint32_t g = k / a.group;
+    const uint32_t h = k % a.group;
+    const uint32_t hd = a.hd;
+    const uint32_t nout = a.group * hd;
+    const uint32_t S = s.n_splits;
+    const float c = a.scale_log2e;
+    const auto pblock = [&](uint32_t j) { return static_cast<std::size_t>(s.block0 + j) * a.n_kv + g; };
+
+    // The head's hd/4 output quads times P parts of the splits fill the
+    // block. The first 8 partial outputs of every thread are loaded before
+    // the weights are known, so both loads overlap.
+    const uint32_t nq = hd / 4;
+    const uint32_t P = 256 / nq;
+    const uint32_t q = tid % nq;
+    const uint32_t part = tid / nq;
+    const float* src = a.part_o + static_cast<std::size_t>(h) * hd + 4 * q;
+    f4 ov[8];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t j = part + i * P;
+        if (part < P && j < S) {
+            ov[i] = *reinterpret_cast<const f4*>(src + pblock(j) * nout);
+        }
+    }
+
+    // Phase 1 (wave 0): lane l holds splits l, l + 64, ...
+    if (tid < 64) {
+        constexpr uint32_t per_lane = decode_max_splits / 64;
+        float mj[per_lane], lj[per_lane];
+        float mx = -INFINITY;
+#pragma unroll
+        for (uint32_t i = 0; i < per_lane; ++i) {
+            const uint32_t j = ln + 64 * i;
+            mj[i] = -INFINITY;
+            lj[i] = 0.0f;
+            if (j < S) {
+                mj[i] = a.part_ml[(pblock(j) * a.group + h) * 2];
+                lj[i] = a.part_ml[(pblock(j) * a.group + h) * 2 + 1];
+            }
+            mx = fmaxf(mx, mj[i]);
+        }
+        mx = wave_max(mx);
+        float sum = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < per_lane; ++i) {
+            mj[i] = fast_exp2((mj[i] - mx) * c);  // 0 for absent splits
+            sum += lj[i] * mj[i];
+        }
+        sum = wave_sum(sum);
+        const float inv = 1.0f / sum;
+#pragma unroll
+        for (uint32_t i = 0; i < per_lane; ++i) {
+            const uint32_t j = ln + 64 * i;
+            if (j < S) {
+                wts[j] = mj[i] * inv;
+            }
+        }
+    }
+    __syncthreads();
+    // Phase 2: out = sum_j w_j O_j, splits in a fixed order per thread.
+    if (part < P) {
+        f4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint32_t j = part + i * P;
+            if (j < S) {
+                acc += wts[j] * ov[i];
+            }
+        }
+        for (uint32_t j = part + 8 * P; j < S; j += 8 * P) {
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                if (j + i * P < S) {
+                    ov[i] = *reinterpret_cast<const f4*>(src + pblock(j + i * P) * nout);
+                }
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                if (j + i * P < S) {
+                    acc += wts[j + i * P] * ov[i];
+                }
+            }
+        }
+        acc_lds[part * nq + q] = acc;
+    }
+    __syncthreads();
+    if (static_cast<uint32_t>(tid) < nq) {
+        f4 sum = acc_lds[tid];
+        for (uint32_t p2 = 1; p2 < P; ++p2) {
+            sum += acc_lds[p2 * nq + tid];
+        }
+        *reinterpret_cast<f4*>(s.out + (static_cast<std::size_t>(g) * a.group + h) * hd + 4 * tid) = sum;
+    }
+}
+
+template <int HDP, bool MULTI>
 hipError_t launch_hdp(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream) {
-    const std::size_t lds = (4 * 16 * 2 + 2 * static_cast<std::size_t>(a.group) * a.hd) * sizeof(float);
+    const std::size_t lds = decode_lds_bytes(a.group, a.hd);
     const dim3 grid(total_splits * a.n_kv);
     if (q_dtype == 1) {
-        decode_kernel<HDP, true><<<grid, 256, lds, stream>>>(a);
+        decode_kernel<HDP, true, MULTI><<<grid, 256, lds, stream>>>(a);
     } else {
-        decode_kernel<HDP, false><<<grid, 256, lds, stream>>>(a);
+        decode_kernel<HDP, false, MULTI><<<grid, 256, lds, stream>>>(a);
+    }
+    if (a.merge_blocks > 0) {
+        decode_merge_kernel<MULTI><<<a.merge_blocks, 256, 0, stream>>>(a);
     }
     return hipGetLastError();
 }
 
+template <int HDP>
+hipError_t launch_hdp(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream) {
+    return a.n_seqs > 1 ? launch_hdp<HDP, true>(a, total_splits, q_dtype, stream)
+                        : launch_hdp<HDP, false>(a, total_splits, q_dtype, stream);
+}
+
 }  // namespace
 
-uint32_t decode_choose_chunk(uint64_t total_positions, uint32_t n_kv) {
+uint32_t decode_choose_chunk(uint64_t total_positions, uint32_t n_kv, uint32_t max_len) {
     // Enough splits to give every CU about one block of 128 positions per
     // KV-head pass; longer runs take longer chunks, which keeps the partials
-    // (and the last block's merge) small against the KV bytes.
+    // (and their merge) small against the KV bytes. No sequence
+    // may have more than decode_max_splits splits.
     const uint64_t work = total_positions * n_kv;
-    uint32_t chunk = decode_chunk_unit;
-    while (chunk < 1024 && work / chunk > 2048) {
+    uint64_t chunk = decode_chunk_unit;
+    while ((chunk < 1024 && work / chunk > 2048) || (uint64_t{max_len} + chunk - 1) / chunk > decode_max_splits) {
         chunk *= 2;
     }
-    return chunk;
+    return static_cast<uint32_t>(chunk);
 }
 
 hipError_t launch_decode(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream) {

@@ -39,6 +39,28 @@ __device__ __forceinline__ void store16(void* p, u4 v) {
     *reinterpret_cast<u4*>(p) = v;
 }
 
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes at
+// g land at lds + 16 * l; lds must be the same for every lane of the wave.
+// Counted by vmcnt like any vector load, and takes no registers.
+__device__ __forceinline__ void load16_lds(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// Raw buffer access: a 128-bit resource (base, byte limit) in scalar
+// registers and a 32-bit per-lane byte offset. A load at or past the limit
+// returns zeros, so a lane with nothing to read just gets an out-of-range
+// offset (buffer_oob). 0x00020000 is the raw-buffer format word on CDNA.
+typedef __amdgpu_buffer_rsrc_t rsrc;
+constexpr uint32_t buffer_oob = 0x80000000u;
+__device__ __forceinline__ rsrc make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+__device__ __forceinline__ u4 buffer_load16(rsrc r, uint32_t offset) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+}
+
 // f32 -> binary16, round to nearest even (v_cvt_f16_f32 in the default mode),
 // the rounding kv_append and attend_group apply (S/numeric/half.hpp:46-82).
 __device__ __forceinline__ _Float16 to_h(float x) {
@@ -61,6 +83,39 @@ __device__ __forceinline__ f16v mfma32(h8 a, h8 b, f16v c) {
 // 2^x on the transcendental unit (v_exp_f32). exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);
+}
+
+// Partner exchange across the wave's 16-lane rows on the VALU (gfx950's
+// v_permlane16_swap / v_permlane32_swap), with no LDS traffic:
+// partner16(v)[l] = v[l ^ 16], partner32(v)[l] = v[l ^ 32].
+// swap16(a, b) returns {a.row0, b.row0, a.row2, b.row2} and
+// {a.row1, b.row1, a.row3, b.row3}; swap32 does the same with 32-lane
+// halves. Each partner is built from two swaps against zero: with the same
+// value in both operands this compiler folds the second result into the
+// first, so the operands are always different.
+__device__ __forceinline__ float partner16(float v) {
+    const unsigned x = __builtin_bit_cast(unsigned, v);
+    const auto lo = __builtin_amdgcn_permlane16_swap(x, 0u, false, false);  // [1] = row above, in even rows
+    const auto hi = __builtin_amdgcn_permlane16_swap(0u, x, false, false);  // [0] = row below, in odd rows
+    return __builtin_bit_cast(float, (__lane_id() & 16) ? hi[0] : lo[1]);
+}
+__device__ __forceinline__ float partner32(float v) {
+    const unsigned x = __builtin_bit_cast(unsigned, v);
+    const auto lo = __builtin_amdgcn_permlane32_swap(x, 0u, false, false);  // [1] = upper half, in the lower
+    const auto hi = __builtin_amdgcn_permlane32_swap(0u, x, false, false);  // [0] = lower half, in the upper
+    return __builtin_bit_cast(float, (__lane_id() & 32) ? hi[0] : lo[1]);
+}
+__device__ __forceinline__ float max16(float v) {
+    return fmaxf(v, partner16(v));
+}
+__device__ __forceinline__ float max32(float v) {
+    return fmaxf(v, partner32(v));
+}
+__device__ __forceinline__ float sum16(float v) {
+    return v + partner16(v);
+}
+__device__ __forceinline__ float sum32(float v) {
+    return v + partner32(v);
 }
 
 __device__ __forceinline__ float xor_max(float v, int mask) {

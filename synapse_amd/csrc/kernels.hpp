@@ -26,32 +26,38 @@ hipError_t launch_kv_append(const kv_layout& c, const void* k_rows, const void* 
 struct decode_seq {
     const void* q;        // n_heads * hd, f32 or f16
     float* out;           // n_heads * hd
-    const _Float16* k;    // K block
-    const _Float16* vt;   // V^T block
+    _Float16* k;          // K block
+    _Float16* vt;         // V^T block
+    const void* k_new;    // the step's new K row (position len-1, n_kv * hd of kv_dtype), or nullptr:
+    const void* v_new;    //   the kernel then stores it into the cache (kv_append) and attends it
     uint32_t len;         // attended positions
     uint32_t ctx_stride;  // V^T row length
     uint32_t block0;      // first split of this sequence in the launch's split numbering
-    uint32_t n_splits;    // ceil(len / chunk)
+    uint32_t n_splits;    // ceil(len / chunk), <= decode_max_splits
+    uint32_t merge0;      // first merge block of this sequence (sequences with one split have none)
 };
 
 constexpr uint32_t decode_max_seqs = 32;  // sequences per launch (kernel-argument table)
 constexpr uint32_t decode_positions_per_wave = 32;
 constexpr uint32_t decode_waves = 4;
 constexpr uint32_t decode_chunk_unit = decode_positions_per_wave * decode_waves;  // 128
+constexpr uint32_t decode_max_splits = 256;  // splits of one sequence (bounds the merge's LDS)
 
 struct decode_args {
     decode_seq seq[decode_max_seqs];
+    uint32_t block0s[decode_max_seqs];  // seq[i].block0, contiguous: a block finds its sequence in one load batch
+    uint32_t merge0s[decode_max_seqs];  // seq[i].merge0, likewise for the merge kernel
     uint32_t n_seqs;
     uint32_t n_kv;
     uint32_t hd;
     uint32_t group;        // query heads per KV head, <= 16
     uint32_t row;          // n_kv * hd: K row length in halves
     uint32_t chunk;        // positions per split, a multiple of decode_chunk_unit
-    uint32_t counter0;     // first merge counter of this launch
+    uint32_t kv_dtype;     // type of k_new / v_new: 0 f32, 1 f16
+    uint32_t merge_blocks; // blocks of the merge kernel: one per (split sequence, query head)
     float scale_log2e;     // scale * log2(e)
     float* part_o;         // [splits * n_kv][group][hd]
     float* part_ml;        // [splits * n_kv][group][2]
-    uint32_t* counters;    // merge counters, zero between launches
 };
 
 // Scratch floats one split contributes: (max, sum, output) for each head.
@@ -60,8 +66,14 @@ inline std::size_t decode_split_floats(uint32_t group, uint32_t hd) {
 }
 
 // Picks the chunk (positions per split) for a launch whose sequences attend
-// `total_positions` positions across n_kv heads.
-uint32_t decode_choose_chunk(uint64_t total_positions, uint32_t n_kv);
+// `total_positions` positions across n_kv heads, the longest `max_len`.
+uint32_t decode_choose_chunk(uint64_t total_positions, uint32_t n_kv, uint32_t max_len);
+
+// The split kernel addresses a split's K rows and a head's V^T rows through
+// 32-bit buffer offsets: both spans must stay below 2^31 bytes.
+inline bool decode_fits(uint32_t chunk, uint32_t row, uint32_t hd, uint32_t ctx_stride) {
+    return uint64_t{chunk} * row * 2 < (uint64_t{1} << 31) && uint64_t{hd} * ctx_stride * 2 < (uint64_t{1} << 31);
+}
 
 hipError_t launch_decode(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream);
 

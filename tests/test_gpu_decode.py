@@ -127,3 +127,29 @@ def test_decode_is_deterministic(arena):
     a, _, _, _ = _case(arena, 32, 8, 128, 6000, seed=5)
     b, _, _, _ = _case(arena, 32, 8, 128, 6000, seed=5)
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("ctx", [0, 127, 128, 4096])
+def test_decode_step_with_f16_rows(arena, ctx):
+    """A step whose new K, V row arrives as binary16 (kv_dtype f16) stores
+    and attends the same halves as the f32 row it rounds from."""
+    n_heads, n_kv, hd = 32, 8, 128
+    cfg = wl.Decode("case", n_heads, n_kv, hd, ctx, 500000.0)
+    kc, vc, q, k, v = wl.decode_inputs(cfg, seed=40 + ctx)
+    k, v = (x.astype(np.float16).astype(np.float32) for x in (k, v))
+    outs, caches = [], []
+    for kv_dtype in (SYN_F32, SYN_F16):
+        mark = arena.top
+        cache = capi.kv_state(arena, ctx + 1, n_kv, hd)
+        if ctx:
+            capi.upload_cache(arena, cache, kc, vc)
+        scratch = scratch_for(arena, n_heads, n_kv, hd, ctx + 1)
+        outs.append(attention(arena, cache, scratch, q, k, v, ctx, n_heads, cfg.scale, kv_dtype=kv_dtype))
+        caches.append(capi.download_cache(arena, cache, ctx + 1))
+        arena.top = mark
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(caches[0][0], caches[1][0]) and np.array_equal(caches[0][1], caches[1][1])
+    ok_k, ok_v = orc.new_cache(ctx + 1, n_kv, hd)
+    ok_k[:ctx], ok_v[:ctx] = kc, vc
+    want = orc.attention_rows(q, k, v, ctx, ok_k, ok_v, n_heads, cfg.scale)
+    assert_close(outs[1], want, what=f"f16 rows ctx {ctx}")

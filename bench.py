@@ -1,18 +1,21 @@
 """Benchmark of the KV-cache attention path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only decode|prefill|ragged|vision]
 
 A step is one decode-attention op of config 2 (Llama-3-8B shape: 32 query
-heads on 8 KV heads, hd 128, 4096 cached rows): append the step's K, V row
-(kv_append) and attend 4097 rows (split-KV decode kernel), through the C ABI.
-Steps rotate over `layers` distinct KV states (>= 512 MiB together, as a
-real model's 32 layers are), so K and V come from HBM, not the 256 MB
-Infinity Cache. Inputs are resident in HBM before the timed region.
+heads on 8 KV heads, hd 128, 4096 cached rows), through the C ABI: the
+split-KV kernel appends the step's K, V row and attends all 4097 rows in
+splits, and the merge kernel combines the splits. Steps rotate over `layers`
+distinct KV states (>= 512 MiB together, as a real model's 32 layers are),
+so K and V come from HBM, not the 256 MB Infinity Cache. Inputs are resident
+in HBM before the timed region.
 
 One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time),
-roofline of the decode kernel (HIP-event kernel time), the CPU oracle timed on
-this host, and the other configs' figures (prefill TFLOP/s, ragged decode,
-ViT) under "extra".
+roofline of the decode op (the same HIP-event time on the arena's stream),
+the CPU oracle timed on this host, and the other configs' figures (prefill
+TFLOP/s, ragged decode, ViT) under "extra". --copy-bytes N adds one arena
+copy of N bytes, the calibration dispatch for rocprofv3 --pmc FETCH_SIZE /
+WRITE_SIZE runs.
 """
 from __future__ import annotations
 
@@ -34,6 +37,10 @@ from synapse_amd import workloads as wl  # noqa: E402
 from synapse_amd.capi import SYN_F16, SYN_F32, Arena, AttnDesc, SelfDesc, SeqDesc, check, lib  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
+# HBM bytes one config-2 decode step moves (split + merge kernels), from two
+# rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a copy of known
+# size; profiles/decode_c2_pmc_traffic.md has the runs and the factors.
+DECODE_TRAFFIC_BYTES = 18_419_688
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 matrix, TFLOP/s
 
 
@@ -241,7 +248,10 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=40, help="distinct KV states rotated over (>= 32)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--decode-only", action="store_true")
+    ap.add_argument("--decode-only", action="store_true", help="same as --only decode")
+    ap.add_argument("--only", choices=["decode", "prefill", "ragged", "vision"], default=None,
+                    help="run one configuration (no JSON line unless it is decode)")
+    ap.add_argument("--copy-bytes", type=int, default=0, help="one arena copy of this many bytes (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention path is built and measured on a single MI355X "
@@ -249,19 +259,14 @@ def main() -> int:
         return 2
 
     hip = Hip()
-    cfg = wl.C2
-    log(f"decode {cfg.name}: {args.steps} steps, {args.warmup} warmup, {args.layers} rotating KV states")
-    step_ms, kern_ms, det = bench_decode(hip, cfg, args.steps, args.warmup, args.layers)
-    nbytes = cfg.kv_bytes()
-    value = nbytes / (step_ms * 1e-3) / 1e9
-    achieved = nbytes / (kern_ms * 1e-3) / 1e9
-    log(f"decode: {step_ms * 1e3:.2f} us/step, kernel {kern_ms * 1e3:.2f} us -> {achieved:.0f} GB/s")
-    extra = {"decode_kernel_us": round(kern_ms * 1e3, 3), "decode_step_us": round(step_ms * 1e3, 3),
-             "decode_tokens_per_s_32_layers": round(1e3 / (step_ms * 32), 1),
-             "decode_wall_us_per_step": round(det["wall_ms_per_step"] * 1e3, 3),
-             "decode_kernel_us_median": round(det["kernel_ms_median"] * 1e3, 3)}
-
-    if not args.decode_only:
+    only = "decode" if args.decode_only else args.only
+    if args.copy_bytes:
+        with Arena(2 * args.copy_bytes + 4096) as arena:
+            check(lib().syn_hip_copy(arena.handle, args.copy_bytes, 0, args.copy_bytes))
+            arena.sync()
+        log(f"copy calibration: {args.copy_bytes} bytes")
+    extra = {}
+    if only in (None, "prefill"):
         p = wl.C3
         log(f"prefill {p.name}")
         kms, op_ms = bench_prefill(hip, p, 50)
@@ -271,18 +276,37 @@ def main() -> int:
                             "op_us_with_append": round(op_ms * 1e3, 2),
                             "tokens_per_s": round(p.n / (op_ms * 1e-3), 0), "flops": p.flops()}
         log(f"prefill: {kms * 1e3:.1f} us, {tf:.0f} TFLOP/s")
+    if only in (None, "ragged"):
         r = wl.C4
         log(f"ragged {r.name}")
         rms, rbytes = bench_ragged(hip, r, 20)
         extra["ragged"] = {"us": round(rms * 1e3, 2), "gbs": round(rbytes / (rms * 1e-3) / 1e9, 1),
                            "frac_of_hbm": round(rbytes / (rms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": rbytes,
                            "seqs_per_s": round(r.n_seqs / (rms * 1e-3), 0)}
+        log(f"ragged: {rms * 1e3:.1f} us, {extra['ragged']['gbs']:.0f} GB/s")
+    if only in (None, "vision"):
         vcfg = wl.C5
         log(f"vision {vcfg.name}")
         vms = bench_vision(hip, vcfg, 50)
         extra["vision"] = {"us": round(vms * 1e3, 2), "tflops": round(vcfg.flops() / (vms * 1e-3) / 1e12, 1),
                            "gbs": round(vcfg.bytes() / (vms * 1e-3) / 1e9, 1),
                            "images_per_s": round(vcfg.batch / (vms * 1e-3), 0)}
+        log(f"vision: {vms * 1e3:.1f} us, {extra['vision']['tflops']:.0f} TFLOP/s")
+    if only not in (None, "decode"):
+        return 0
+
+    cfg = wl.C2
+    log(f"decode {cfg.name}: {args.steps} steps, {args.warmup} warmup, {args.layers} rotating KV states")
+    step_ms, kern_ms, det = bench_decode(hip, cfg, args.steps, args.warmup, args.layers)
+    nbytes = cfg.kv_bytes()
+    value = nbytes / (step_ms * 1e-3) / 1e9
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    log(f"decode: {step_ms * 1e3:.2f} us/step -> {value:.0f} GB/s")
+    extra.update({"decode_step_us": round(step_ms * 1e3, 3),
+                  "decode_tokens_per_s_32_layers": round(1e3 / (step_ms * 32), 1),
+                  "decode_wall_us_per_step": round(det["wall_ms_per_step"] * 1e3, 3),
+                  "decode_single_step_us_median": round(det["kernel_ms_median"] * 1e3, 3),
+                  "decode_kernels_per_step": 2})
 
     line = {
         "metric": "decode attn HBM GB/s (8B GQA, KV 4k) + prefill attn TFLOP/s; % roofline",
@@ -293,7 +317,8 @@ def main() -> int:
                                "+ 1 appended (append + attend per step)",
                    "kv_states_rotated": args.layers, "bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
+                     "kernel": "decode op (split-KV kernel + merge kernel), HIP events over the timed region"},
         "cpu_baseline": None,
         "extra": extra,
     }

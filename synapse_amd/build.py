@@ -72,24 +72,23 @@ def build_oracle() -> None:
 
 
 CPP_TESTS = {
-    # name: (source, needs the HIP library)
+    # name: (source, links the CPU oracle)
     "test_graph": ("tests/cpp/test_graph.cpp", False),
     "test_session": ("tests/cpp/test_session.cpp", True),
 }
 
 
 def build_host_tests() -> None:
+    """The C++20 host tests: both link libsynapse_hip.so (the builder sizes
+    attention scratch through it); the session test also links the oracle."""
     out = ROOT / "tests" / "cpp" / "_bin"
     out.mkdir(parents=True, exist_ok=True)
-    for name, (src, hip) in CPP_TESTS.items():
-        path = ROOT / src
-        if not path.exists():
-            continue
-        cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-Wextra", "-Werror", "-ffp-contract=off",
-               f"-I{HOST_INC}", f"-I{ROOT / 'include'}", f"-I{ROOT / 'oracle'}", str(path), "-o", str(out / name)]
-        if hip:
-            cmd += [f"-L{PKG}", "-lsynapse_hip", f"-Wl,-rpath,{PKG}", f"-L{ROOT / 'oracle'}", "-loracle",
-                    f"-Wl,-rpath,{ROOT / 'oracle'}", "-pthread"]
+    for name, (src, oracle) in CPP_TESTS.items():
+        cmd = ["g++", "-std=c++20", "-O2", "-Wall", "-Wextra", "-Werror", "-ffp-contract=off", f"-I{HOST_INC}",
+               f"-I{ROOT / 'include'}", f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / src), "-o", str(out / name),
+               f"-L{PKG}", "-lsynapse_hip", f"-Wl,-rpath,{PKG}", "-pthread"]
+        if oracle:
+            cmd += [f"-I{ROOT / 'oracle'}", f"-L{ROOT / 'oracle'}", "-loracle", f"-Wl,-rpath,{ROOT / 'oracle'}"]
         _run(cmd)
 
 

@@ -1,0 +1,252 @@
+// session.hpp — executes a compute_graph on one MI355X through the C ABI
+// (include/synapse_hip.h). The reference's session (S/graph/session.hpp:
+// 82-467) owns a host arena laid out by the static plan plus the KV states;
+// this one owns a device arena laid out the same way:
+//
+//   [ planned tensors: plan(g), 256-byte aligned ][ RoPE frequency tables ]
+//   [ KV state 0 ][ KV state 1 ] ...   (each syn_hip_kv_state_bytes, aligned)
+//
+// one syn_hip_arena_create at construction and nothing allocated afterwards.
+// run(batch) keeps the reference's contract (S/graph/session.hpp:143-177):
+// it returns false and runs nothing unless 1 <= n <= max_batch and
+// pos + n <= position_limit; otherwise it executes every node in graph order
+// on the arena's stream -- op_rope through syn_hip_rope, op_attention through
+// syn_hip_attention (the drop-in for execute(op_attention), :348-374) and
+// op_self_attention through syn_hip_self_attention (execute(op_self_attention),
+// :409-449). Inputs are written and outputs read with write()/read(), the
+// device counterparts of tensor(t) (:107-110). A HIP failure during a run
+// stops it, returns false and is kept in status().
+#pragma once
+
+#include "graph.hpp"
+#include "planner.hpp"
+
+#include <span>
+
+namespace syn::graph {
+
+struct step {  // S/graph/session.hpp: one token at a position
+    std::uint32_t token = 0;
+    std::uint32_t pos = 0;
+};
+
+struct batch {  // tokens.size() consecutive tokens, the first at pos
+    std::span<const std::uint32_t> tokens;
+    std::uint32_t pos = 0;
+};
+
+class session {
+public:
+    explicit session(const compute_graph& g) : graph_(&g), plan_(plan(g)) {
+        std::size_t top = plan_.arena_bytes;
+        const auto& nodes = g.nodes();
+        const_offset_.assign(nodes.size(), ~std::uint64_t{0});
+        for (std::size_t i = 0; i < nodes.size(); ++i) {
+            if (const auto* r = std::get_if<op_rope>(&nodes[i]); r && !r->freq_factors.empty()) {
+                const_offset_[i] = top;
+                top = align_up(top + r->freq_factors.size() * sizeof(float));
+            }
+        }
+        const std::size_t states_begin = top;
+        for (const state_desc& s : g.states()) {
+            const auto max_ctx = static_cast<std::uint32_t>(s.max_ctx);
+            const auto n_kv = static_cast<std::uint32_t>(s.n_kv_heads);
+            const auto hd = static_cast<std::uint32_t>(s.head_dim);
+            const std::uint64_t k_bytes = align_up(std::size_t{max_ctx} * n_kv * hd * 2);
+            kv_.push_back(syn_kv_desc{top, top + k_bytes, max_ctx, n_kv, hd, syn_hip_kv_ctx_stride(max_ctx)});
+            top = align_up(top + syn_hip_kv_state_bytes(max_ctx, n_kv, hd));
+        }
+        state_bytes_ = top - states_begin;
+        status_ = syn_hip_arena_create(std::max<std::size_t>(top, plan_alignment), &arena_);
+        if (status_ != SYN_HIP_OK) {
+            arena_ = nullptr;
+            return;
+        }
+        for (std::size_t i = 0; i < nodes.size() && status_ == SYN_HIP_OK; ++i) {
+            if (const_offset_[i] != ~std::uint64_t{0}) {
+                const auto& ff = std::get<op_rope>(nodes[i]).freq_factors;
+                status_ = syn_hip_upload(arena_, const_offset_[i], ff.data(), ff.size() * sizeof(float));
+            }
+        }
+        reset();
+    }
+    session(const compute_graph&&) = delete;  // the graph must outlive the session
+    session(const session&) = delete;
+    session& operator=(const session&) = delete;
+    ~session() {
+        (void)syn_hip_arena_destroy(arena_);
+    }
+
+    // SYN_HIP_OK, or why construction or the last run failed.
+    int status() const noexcept {
+        return status_;
+    }
+    const memory_plan& memory() const noexcept {
+        return plan_;
+    }
+    // Device bytes held by the KV states.
+    std::size_t state_bytes() const noexcept {
+        return state_bytes_;
+    }
+    syn_arena* arena() noexcept {
+        return arena_;
+    }
+    std::uint64_t offset(tensor_id t) const noexcept {
+        return plan_.offset[t];
+    }
+    const syn_kv_desc& state(state_id s) const noexcept {
+        return kv_[s];
+    }
+
+    // Writes the first rows of tensor t (an input) from host floats.
+    bool write(tensor_id t, std::span<const float> rows) noexcept {
+        if (!usable(t, rows.size())) {
+            return false;
+        }
+        return keep(syn_hip_upload(arena_, plan_.offset[t], rows.data(), rows.size_bytes()));
+    }
+    // Reads the first rows of tensor t (after the run that wrote them).
+    bool read(tensor_id t, std::span<float> rows) noexcept {
+        if (!usable(t, rows.size())) {
+            return false;
+        }
+        return keep(syn_hip_download(arena_, plan_.offset[t], rows.data(), rows.size_bytes()));
+    }
+
+    // Zeroes every state, as before a new sequence (S/graph/session.hpp:127-129).
+    void reset() noexcept {
+        if (arena_ != nullptr && state_bytes_ > 0) {
+            keep(syn_hip_fill(arena_, kv_.front().k_offset, 0, state_bytes_));
+        }
+    }
+
+    [[nodiscard]] bool run(step s = {}) noexcept {
+        return run(batch{std::span<const std::uint32_t>(&s.token, 1), s.pos});
+    }
+
+    [[nodiscard]] bool run(batch b) noexcept {
+        const std::size_t n = b.tokens.size();
+        if (!accepts(n, b.pos)) {
+            return false;
+        }
+        return execute_all(n, 1, b.pos);
+    }
+
+    // n rows at position 0, one image (S/graph/session.hpp:164-171).
+    [[nodiscard]] bool run_rows(std::size_t n) noexcept {
+        if (!accepts(n, 0)) {
+            return false;
+        }
+        return execute_all(n, 1, 0);
+    }
+
+    // GPU extension: `images` independent images of `rows` rows each in one
+    // run (rows * images <= max_batch); self-attention stays within an image.
+    // The reference encodes one image per run_rows call (S/models/clip.hpp:410).
+    [[nodiscard]] bool run_images(std::size_t rows, std::size_t images) noexcept {
+        if (images == 0 || rows > graph_->max_batch() / std::max<std::size_t>(images, 1) || !accepts(rows * images, 0)) {
+            return false;
+        }
+        return execute_all(rows, images, 0);
+    }
+
+private:
+    bool accepts(std::size_t n, std::uint32_t pos) const noexcept {
+        return arena_ != nullptr && n != 0 && n <= graph_->max_batch() &&
+               std::size_t{pos} + n <= graph_->position_limit();
+    }
+
+    bool usable(tensor_id t, std::size_t floats) const noexcept {
+        return arena_ != nullptr && t < graph_->tensors().size() &&
+               graph_->tensors()[t].role != tensor_role::scratch &&
+               floats <= graph_->rows(t) * graph_->tensors()[t].size;
+    }
+
+    bool keep(int status) noexcept {
+        if (status != SYN_HIP_OK) {
+            status_ = status;
+        }
+        return status == SYN_HIP_OK;
+    }
+
+    bool execute_all(std::size_t rows, std::size_t images, std::uint32_t pos) noexcept {
+        const auto& nodes = graph_->nodes();
+        for (std::size_t i = 0; i < nodes.size(); ++i) {
+            const int e = std::visit([&](const auto& op) { return execute(op, i, rows, images, pos); }, nodes[i]);
+            if (!keep(e)) {
+                return false;
+            }
+        }
+        return true;
+    }
+
+    int execute(const op_rope& r, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t pos) noexcept {
+        const std::size_t size = graph_->tensors()[r.in].size;
+        for (std::size_t img = 0; img < images; ++img) {
+            syn_rope_desc d{};
+            d.in_offset = plan_.offset[r.in] + img * rows * size * sizeof(float);
+            d.out_offset = plan_.offset[r.out] + img * rows * size * sizeof(float);
+            d.freq_factors_offset = const_offset_[i];
+            d.n = static_cast<std::uint32_t>(rows);
+            d.size = static_cast<std::uint32_t>(size);
+            d.head_dim = static_cast<std::uint32_t>(r.head_dim);
+            d.pos = pos;
+            d.theta_scale = r.theta_scale;
+            d.mode = r.mode == rope_mode::neox ? 1u : 0u;
+            d.freq_scale = r.scaling.freq_scale;
+            d.ext_factor = r.scaling.ext_factor;
+            d.attn_factor = r.scaling.attn_factor;
+            d.corr_low = r.scaling.corr_low;
+            d.corr_high = r.scaling.corr_high;
+            if (const int e = syn_hip_rope(arena_, &d)) {
+                return e;
+            }
+        }
+        return SYN_HIP_OK;
+    }
+
+    int execute(const op_attention& a, std::size_t, std::size_t rows, std::size_t, std::uint32_t pos) noexcept {
+        syn_attn_desc d{};
+        d.cache = kv_[a.cache];
+        d.q_offset = plan_.offset[a.q];
+        d.k_offset = plan_.offset[a.k];
+        d.v_offset = plan_.offset[a.v];
+        d.out_offset = plan_.offset[a.out];
+        d.scratch_offset = plan_.offset[a.scratch];
+        d.scratch_bytes = graph_->tensors()[a.scratch].bytes;
+        d.n_heads = static_cast<std::uint32_t>(a.n_heads);
+        d.pos = pos;
+        d.n = static_cast<std::uint32_t>(rows);
+        d.scale = a.scale;
+        d.q_dtype = SYN_F32;
+        d.kv_dtype = SYN_F32;
+        return syn_hip_attention(arena_, &d);
+    }
+
+    int execute(const op_self_attention& s, std::size_t, std::size_t rows, std::size_t images,
+                std::uint32_t) noexcept {
+        const std::size_t size = graph_->tensors()[s.q].size;
+        syn_self_desc d{};
+        d.q_offset = plan_.offset[s.q];
+        d.k_offset = plan_.offset[s.k];
+        d.v_offset = plan_.offset[s.v];
+        d.out_offset = plan_.offset[s.out];
+        d.n = static_cast<std::uint32_t>(rows);
+        d.batch = static_cast<std::uint32_t>(images);
+        d.n_heads = static_cast<std::uint32_t>(s.n_heads);
+        d.head_dim = static_cast<std::uint32_t>(size / s.n_heads);
+        d.scale = s.scale;
+        d.in_dtype = SYN_F32;
+        return syn_hip_self_attention(arena_, &d);
+    }
+
+    const compute_graph* graph_;
+    memory_plan plan_;
+    std::vector<std::uint64_t> const_offset_;  // per node: its RoPE table, or ~0
+    std::vector<syn_kv_desc> kv_;
+    std::size_t state_bytes_ = 0;
+    syn_arena* arena_ = nullptr;
+    int status_ = SYN_HIP_OK;
+};
+
+}  // namespace syn::graph

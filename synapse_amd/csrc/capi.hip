@@ -273,7 +273,8 @@ int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows) {
                           d->scratch_offset, d->scratch_bytes);
     }
     const syn::flash_args f = flash_of(a, d);
-    if (fast_shape(c.head_dim)) {
+    if (fast_shape(c.head_dim) && (uint64_t{d->n} + 127) / 128 <= 65535 &&
+        syn::prefill_fits(d->pos + d->n, c.n_kv_heads * c.head_dim, c.head_dim, c.ctx_stride)) {
         return hip_status(syn::launch_prefill(f, d->q_dtype, a->stream), "prefill launch");
     }
     return hip_status(syn::launch_generic_causal(f, d->q_dtype, a->stream), "generic causal launch");

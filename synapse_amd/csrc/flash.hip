@@ -1,16 +1,12 @@
-// flash.hip — tiled attention on the f16 matrix cores: causal prefill over
-// the KV cache, and bidirectional (image encoder) attention over rows.
+// flash.hip — bidirectional (image encoder) attention over rows on the f16
+// matrix cores: session::execute(op_self_attention) (S/graph/session.hpp:
+// 409-449) with self_attend_head's math (S/kernels/attention.hpp:460-486),
+// for `batch` independent images of n rows each.
 //
-// Causal: session::execute(op_attention) for a run of n tokens at positions
-// pos..pos+n-1 (S/graph/session.hpp:348-374): token i attends cache rows
-// 0..pos+i with attend_group's math (S/kernels/attention.hpp:185-244).
-// Bidirectional: session::execute(op_self_attention) (S/graph/session.hpp:
-// 409-449) with self_attend_head's math (S/kernels/attention.hpp:460-486).
-//
-// A block (4 waves) owns 128 queries of one head; wave w owns 32 of them. Key
-// tiles of 64 keys are staged in LDS (K rows as stored; V transposed, which
-// the cache already is) and shared by the 4 waves. Per 32-key slice a wave
-// computes
+// A block (4 waves) owns 128 queries of one head of one image; wave w owns 32
+// of them. Key tiles of 64 keys are staged in LDS (K rows as given; V rows
+// transposed on the way in) and shared by the 4 waves. Per 32-key slice a
+// wave computes
 //   S^T (32 keys x 32 queries) = K (32 x hd) . Q^T          hd/16 MFMA 32x32x16
 //   O^T (32 dims x 32 queries) += V^T (32 x 16 keys) . P^T   per 16 keys and 32 dims
 // With S^T, a query's scores sit in one lane (two, across the lane halves),
@@ -19,8 +15,8 @@
 // a permuted order so that the S^T accumulator registers are, unchanged, the
 // P^T operand of the second product (lane half H holds keys 8H..8H+7 of each
 // 16-key step). Scores stay raw q.k; scale and log2(e) fold into one
-// multiply before exp2. P is rounded to f16 for the matrix cores, as the
-// reference rounds p (S/kernels/attention.hpp:225-227).
+// multiply before exp2. Operands and P are binary16 for the matrix cores
+// (the reference keeps f32 here; the difference is within the parity bound).
 
 #include "kernels.hpp"
 
@@ -58,16 +54,14 @@ __device__ __forceinline__ u4 load8_as_h(const void* base, std::size_t index) {
     }
 }
 
-// SRC: 0 = causal over the KV cache (K rows + V^T); 1 = bidirectional over
-// rows (K and V rows of type IN).
-template <int HD, int SRC, bool QF16>
+// K and V rows of type QF16 ? f16 : f32.
+template <int HD, bool QF16>
 __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
     constexpr int NS = HD / 16;       // k-steps of the score product
     constexpr int NT = HD / 32;       // 32-dim tiles of the output
     constexpr int HSPAN = HD / 2;     // dims a lane half holds across the k-steps
     constexpr int KROW = HD + kpad;   // LDS K row (halves)
     constexpr int VROW = bk + kpad;   // LDS V^T row (halves)
-    constexpr bool causal = SRC == 0;
     __shared__ __attribute__((aligned(16))) _Float16 lk[bk * KROW];
     __shared__ __attribute__((aligned(16))) _Float16 lv[HD * VROW];
 
@@ -77,9 +71,7 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
     const int H = ln >> 5;   // lane half
     const int qi = ln & 31;  // query column of this lane
     const uint32_t hd = a.hd;
-    const uint32_t n_tiles = gridDim.x;
-    // Causal blocks run heaviest (latest) query tiles first.
-    const uint32_t qt = causal ? n_tiles - 1 - blockIdx.x : blockIdx.x;
+    const uint32_t qt = blockIdx.x;
     const uint32_t h = blockIdx.y;
     const uint32_t img = blockIdx.z;
     const uint32_t g = h / a.group;
@@ -113,11 +105,7 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
     }
     float m_run = -INFINITY, l_run = 0.0f;
 
-    // Keys this block needs: causal stops at its last query's position.
-    const uint32_t q_last_block = min(a.n, q_first + bq) - 1;
-    const uint32_t kv_end = causal ? min(a.kv_len, a.pos + q_last_block + 1) : a.kv_len;
-    const uint32_t wave_last_pos = a.pos + min(a.n - 1, q_row0 + 31);  // causal horizon of the wave
-    const uint32_t my_pos = a.pos + my_q;
+    const uint32_t kv_end = a.kv_len;
 
     for (uint32_t t0 = 0; t0 < kv_end; t0 += bk) {
         __syncthreads();  // the previous tile is no longer read
@@ -130,38 +118,11 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
             const uint32_t key = t0 + kr;
             u4 v = zero_u4();
             if (key < kv_end && k8 * 8 < static_cast<int>(hd)) {
-                if constexpr (SRC == 0) {
-                    v = load16(a.k + static_cast<std::size_t>(key) * a.row + g * hd + k8 * 8);
-                } else {
-                    v = load8_as_h<QF16>(a.k_rows, (row_base + key) * a.row + g * hd + k8 * 8);
-                }
+                v = load8_as_h<QF16>(a.k_rows, (row_base + key) * a.row + g * hd + k8 * 8);
             }
             *reinterpret_cast<u4*>(lk + kr * KROW + k8 * 8) = v;
         }
-        if constexpr (SRC == 0) {
-            constexpr int vchunks = HD * (bk / 8);
-#pragma unroll
-            for (int cidx = tid; cidx < vchunks; cidx += 256) {
-                const int d = cidx / (bk / 8);
-                const int k8 = cidx % (bk / 8);
-                const uint32_t key = t0 + k8 * 8;
-                u4 v = zero_u4();
-                if (key < kv_end && d < static_cast<int>(hd)) {
-                    v = load16(a.vt + static_cast<std::size_t>(g * hd + d) * a.ctx_stride + key);
-                    if (key + 8 > kv_end) {
-                        h8 hv = as_h8(v);
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            if (key + j >= kv_end) {
-                                hv[j] = 0;
-                            }
-                        }
-                        v = as_u4(hv);
-                    }
-                }
-                *reinterpret_cast<u4*>(lv + d * VROW + k8 * 8) = v;
-            }
-        } else {
+        {
             // V rows -> V^T: each thread reads 8 dims of one key and scatters them.
             constexpr int vchunks = bk * (HD / 8);
 #pragma unroll
@@ -182,9 +143,6 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
         }
         __syncthreads();
 
-        if (causal && t0 > wave_last_pos) {
-            continue;  // every key of the tile is after every query of this wave
-        }
         if (q_row0 >= a.n) {
             continue;  // a wave past the last query
         }
@@ -211,7 +169,7 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const uint32_t key = t0 + 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
-                const bool masked = key >= kv_end || (causal && key > my_pos);
+                const bool masked = key >= kv_end;
                 if (masked) {
                     sc[e][i] = -INFINITY;
                 }
@@ -274,49 +232,40 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
     }
 }
 
-template <int HD, int SRC>
+template <int HD>
 hipError_t launch_hd(const flash_args& a, uint32_t dtype, hipStream_t stream) {
     const dim3 grid((a.n + bq - 1) / bq, a.n_heads, a.batch);
     if (dtype == 1) {
-        flash_kernel<HD, SRC, true><<<grid, 256, 0, stream>>>(a);
+        flash_kernel<HD, true><<<grid, 256, 0, stream>>>(a);
     } else {
-        flash_kernel<HD, SRC, false><<<grid, 256, 0, stream>>>(a);
+        flash_kernel<HD, false><<<grid, 256, 0, stream>>>(a);
     }
     return hipGetLastError();
 }
 
-template <int SRC>
-hipError_t launch_any(const flash_args& a, uint32_t dtype, hipStream_t stream) {
+}  // namespace
+
+hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream) {
     switch ((a.hd + 31) / 32 * 32) {
     case 32:
-        return launch_hd<32, SRC>(a, dtype, stream);
+        return launch_hd<32>(a, in_dtype, stream);
     case 64:
-        return launch_hd<64, SRC>(a, dtype, stream);
+        return launch_hd<64>(a, in_dtype, stream);
     case 96:
-        return launch_hd<96, SRC>(a, dtype, stream);
+        return launch_hd<96>(a, in_dtype, stream);
     case 128:
-        return launch_hd<128, SRC>(a, dtype, stream);
+        return launch_hd<128>(a, in_dtype, stream);
     case 160:
-        return launch_hd<160, SRC>(a, dtype, stream);
+        return launch_hd<160>(a, in_dtype, stream);
     case 192:
-        return launch_hd<192, SRC>(a, dtype, stream);
+        return launch_hd<192>(a, in_dtype, stream);
     case 224:
-        return launch_hd<224, SRC>(a, dtype, stream);
+        return launch_hd<224>(a, in_dtype, stream);
     case 256:
-        return launch_hd<256, SRC>(a, dtype, stream);
+        return launch_hd<256>(a, in_dtype, stream);
     default:
         return hipErrorInvalidValue;
     }
-}
-
-}  // namespace
-
-hipError_t launch_prefill(const flash_args& a, uint32_t q_dtype, hipStream_t stream) {
-    return launch_any<0>(a, q_dtype, stream);
-}
-
-hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream) {
-    return launch_any<1>(a, in_dtype, stream);
 }
 
 }  // namespace syn

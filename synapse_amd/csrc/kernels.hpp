@@ -98,6 +98,9 @@ struct flash_args {
     float scale_log2e;
 };
 
+// Causal prefill over the cache (prefill.hip). Its buffer resources span the
+// K rows up to kv_len and a head's V^T rows: both must stay below 2^31 bytes.
+bool prefill_fits(uint32_t kv_len, uint32_t row, uint32_t hd, uint32_t ctx_stride);
 hipError_t launch_prefill(const flash_args& a, uint32_t q_dtype, hipStream_t stream);
 hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream);
 

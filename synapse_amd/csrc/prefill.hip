@@ -1,0 +1,356 @@
+// prefill.hip — causal attention of a run of n tokens over the KV cache, on
+// the f16 matrix cores.
+//
+// session::execute(op_attention) for tokens at positions pos..pos+n-1
+// (S/graph/session.hpp:348-374): token i attends cache rows 0..pos+i with
+// attend_group's math (S/kernels/attention.hpp:185-244), the run's own rows
+// already appended.
+//
+// A block (4 waves) owns 128 queries of one head, a wave 32 of them. Key
+// tiles of 64 keys pass through LDS in two stages, copied straight from
+// global memory (buffer_load ... lds, no registers): while the waves compute
+// tile t from one stage, tile t+1's copy is landing in the other. Per 32-key
+// slice a wave computes
+//   S^T (32 keys x 32 queries) = K (32 x hd) . Q^T          hd/16 MFMA 32x32x16
+//   O^T (32 dims x 32 queries) += V^T (32 x 16 keys) . P^T   per 16 keys and 32 dims
+// K rows are loaded in a permuted order so the S^T accumulators are, as they
+// stand, the P^T operand; a query's scores sit in one lane (two across the
+// lane halves), so the row max and sum are in-lane plus one exchange. Only
+// tiles that cross a wave's diagonal (or the end) are masked.
+
+#include "kernels.hpp"
+
+namespace syn {
+
+namespace {
+
+constexpr int pf_bq = 128;  // queries per block
+constexpr int pf_bk = 64;   // keys per LDS tile
+
+// Key offset (inside a 32-key slice) that S^T accumulator row m holds.
+__device__ __forceinline__ int pf_slice_key(int m) {
+    return 16 * (m >> 4) + 8 * ((m >> 2) & 1) + 4 * ((m >> 3) & 1) + (m & 3);
+}
+
+// s_waitcnt immediate: at most n vector memory operations outstanding
+// (vmcnt split over bits 3:0 and 15:14; expcnt, lgkmcnt not waited on).
+constexpr int pf_vmcnt(int n) {
+    return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+}
+
+// Workgroup barrier for the tile pipeline. __syncthreads() carries a release
+// fence that waits for every outstanding vector memory operation, the tile
+// copy just issued for the other stage included; here each wave waits for
+// its own copies with s_waitcnt vmcnt before this barrier, so the barrier only
+// needs the LDS operations (reads of the stage about to be refilled, the tail
+// fix-up writes) complete. The asm's memory clobber keeps the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void pf_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <bool F16>
+__device__ __forceinline__ h8 pf_load_q(const void* base, std::size_t index) {
+    if constexpr (F16) {
+        return as_h8(load16(static_cast<const _Float16*>(base) + index));
+    } else {
+        const float* p = static_cast<const float*>(base) + index;
+        const f4 lo = *reinterpret_cast<const f4*>(p);
+        const f4 hi = *reinterpret_cast<const f4*>(p + 4);
+        return h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]), to_h(hi[0]), to_h(hi[1]), to_h(hi[2]),
+                  to_h(hi[3])};
+    }
+}
+
+template <int HD, bool QF16>
+__global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const flash_args a) {
+    constexpr int NS = HD / 16;     // k-steps of the score product
+    constexpr int NT = HD / 32;     // 32-dim tiles of the output
+    constexpr int HSPAN = HD / 2;   // dims a lane half holds across the k-steps
+    constexpr int KCPR = HD / 8;               // 16-byte chunks of a K row
+    constexpr int KROWC = KCPR + 1;            // LDS K row: one chunk of padding
+    constexpr int VROWC = pf_bk / 8 + 1;       // LDS V^T row: 8 chunks of keys + padding
+    constexpr int TK = pf_bk * KROWC / 64;     // 1 KB copies per K tile (exact)
+    constexpr int TV = (HD * VROWC + 63) / 64; // 1 KB copies per V^T tile (last one partly slack)
+    constexpr int TT = TK + TV;
+    // Two LDS stages, separate objects so the compiler can tell a copy into
+    // one from reads of the other.
+    __shared__ __attribute__((aligned(16))) char lk0[TK * 1024];
+    __shared__ __attribute__((aligned(16))) char lk1[TK * 1024];
+    __shared__ __attribute__((aligned(16))) char lv0[TV * 1024];
+    __shared__ __attribute__((aligned(16))) char lv1[TV * 1024];
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int ln = tid & 63;
+    const int H = ln >> 5;   // lane half
+    const int qi = ln & 31;  // query column of this lane
+    const uint32_t hd = a.hd;
+    // Block -> (query tile, head): heads fastest; the first half of the grid
+    // takes the latest (heaviest) query tiles in descending order, the second
+    // half the earliest in ascending order, so the blocks resident together
+    // on a CU carry about equal causal work.
+    const uint32_t n_qt = (a.n + pf_bq - 1) / pf_bq;
+    const uint32_t rank = blockIdx.x / a.n_heads;
+    const uint32_t h = blockIdx.x % a.n_heads;
+    const uint32_t heavy = (n_qt + 1) / 2;
+    const uint32_t qt = rank < heavy ? n_qt - 1 - rank : rank - heavy;
+    const uint32_t g = h / a.group;
+    const float c = a.scale_log2e;
+
+    const uint32_t q_first = qt * pf_bq;
+    const uint32_t q_row0 = q_first + 32 * w;
+    const uint32_t my_q = q_row0 + qi;
+    const uint32_t my_pos = a.pos + my_q;
+    const uint32_t q_last_block = min(a.n, q_first + pf_bq) - 1;
+    const uint32_t kv_end = min(a.kv_len, a.pos + q_last_block + 1);  // keys this block needs
+    const uint32_t wave_last_pos = a.pos + min(a.n - 1, q_row0 + 31);  // causal horizon of the wave
+    const uint32_t n_tiles = (kv_end + pf_bk - 1) / pf_bk;
+
+    // Q^T operand for the whole block: lane (H, qi) holds query my_q, dims
+    // H*HSPAN + 8*st + [0, 8), rounded to binary16 (S/kernels/attention.hpp:204-206).
+    h8 qv[NS];
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        const uint32_t d0 = H * HSPAN + 8 * st;
+        qv[st] = my_q < a.n && d0 < hd ? pf_load_q<QF16>(a.q, static_cast<std::size_t>(my_q) * a.q_row + h * hd + d0)
+                                       : as_h8(zero_u4());
+    }
+
+    // Tile copies, global -> LDS through buffer resources, 1 KB per wave
+    // instruction (buffer_load ... lds writes lane l's 16 bytes at +16 l):
+    // keys at or past kv_end and dims past hd arrive as zeros. LDS rows carry
+    // one 16-byte chunk of padding (K: 64 rows of KCPR + 1 chunks; V^T: HD rows
+    // of 8 + 1), so the operand reads below spread over the banks; a lane whose
+    // slot is padding, or slack past the V^T rows, copies an out-of-range zero.
+    // Copy j of a tile goes to wave j % 4.
+    const rsrc k_res = make_rsrc(a.k + g * hd, kv_end * a.row * 2 - g * hd * 2);
+    const rsrc v_res = make_rsrc(a.vt + static_cast<std::size_t>(g) * hd * a.ctx_stride, hd * a.ctx_stride * 2);
+    const auto issue = [&](uint32_t t0, char* sk, char* sv) {
+#pragma unroll
+        for (int i = 0; i < (TT + 3) / 4; ++i) {
+            const uint32_t j = w + 4 * i;
+            if (j < TK) {
+                const uint32_t L = 64 * j + ln;
+                const uint32_t r = L / KROWC, cc = L % KROWC;
+                const uint32_t key = t0 + r;
+                const uint32_t off = key < kv_end && cc < KCPR && 8 * cc < hd ? key * a.row * 2 + cc * 16 : buffer_oob;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    k_res, (__attribute__((address_space(3))) void*)(sk + 1024 * j), 16, off, 0, 0, 0);
+            } else if (j < TT) {
+                const uint32_t L = 64 * (j - TK) + ln;
+                const uint32_t d = L / VROWC, cc = L % VROWC;
+                const uint32_t key = t0 + 8 * cc;
+                const uint32_t off = key < kv_end && cc < 8 && d < hd ? d * a.ctx_stride * 2 + key * 2 : buffer_oob;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    v_res, (__attribute__((address_space(3))) void*)(sv + 1024 * (j - TK)), 16, off, 0, 0, 0);
+            }
+        }
+    };
+    // The last tile's V^T chunk that straddles kv_end holds stale halves past
+    // it (a zero probability times a stale non-finite half would be NaN): zero them.
+    const auto fixup = [&](uint32_t t0, char* sv) {
+        if (kv_end % 8 != 0 && tid < HD) {
+            _Float16* chunk = reinterpret_cast<_Float16*>(sv + (tid * VROWC + (kv_end - t0) / 8) * 16);
+            for (uint32_t j = kv_end % 8; j < 8; ++j) {
+                chunk[j] = 0;
+            }
+        }
+    };
+
+    f16v o[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            o[n][i] = 0.0f;
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // One 64-key tile from one LDS stage.
+    const auto compute = [&](uint32_t t0, const char* sk, const char* sv) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (q_row0 >= a.n || t0 > wave_last_pos) {
+            return;  // every key of the tile is after every query of this wave
+        }
+        f16v sc[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                sc[e][i] = 0.0f;
+            }
+            const char* krow = sk + ((32 * e + pf_slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
+            }
+        }
+        // Register i of slice e holds key t0 + 32e + 16(i/8) + 8H + i%8.
+        float tmax = -INFINITY;
+        const bool diagonal = t0 + pf_bk - 1 > a.pos + q_row0 || t0 + pf_bk > kv_end;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (diagonal) {
+                    const uint32_t key = t0 + 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
+                    if (key > my_pos || key >= kv_end) {
+                        sc[e][i] = -INFINITY;
+                    }
+                }
+                tmax = fmaxf(tmax, sc[e][i]);
+            }
+        }
+        tmax = max32(tmax);
+        const float m_new = fmaxf(m_run, tmax);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = fast_exp2((m_run - m_use) * c);
+        m_run = m_new;
+        h8 pv[4];  // P^T operands: 16-key steps 0..3 of the tile
+        float psum = 0.0f;
+        const float mc = m_use * c;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const _Float16 ph = to_h(fast_exp2(sc[e][i] * c - mc));
+                pv[2 * e + (i >> 3)][i & 7] = ph;
+                psum += static_cast<float>(ph);
+            }
+        }
+        l_run = l_run * alpha + sum32(psum);
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                o[n][i] *= alpha;
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const char* vrow = sv + ((32 * n + qi) * VROWC + H) * 16;  // V^T row 32n + qi, keys 8H..
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                o[n] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[n]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Pipeline over tiles, two stages: tile t computes from one stage while
+    // tile t+1's copy lands in the other; a stage is refilled (tile t+2)
+    // once every wave has finished reading it.
+    // This wave's copies per tile: TT / 4 or one more.
+    const uint32_t per_tile = (TT - w + 3) / 4;
+    const auto wait_tile = [&](uint32_t next_issued) {
+        if (!next_issued) {
+            __builtin_amdgcn_s_waitcnt(pf_vmcnt(0));
+        } else if (per_tile == (TT + 3) / 4) {
+            __builtin_amdgcn_s_waitcnt(pf_vmcnt((TT + 3) / 4));
+        } else {
+            __builtin_amdgcn_s_waitcnt(pf_vmcnt(TT / 4));
+        }
+    };
+    issue(0, lk0, lv0);
+    if (n_tiles > 1) {
+        issue(pf_bk, lk1, lv1);
+    }
+    wait_tile(n_tiles > 1);
+    pf_barrier();
+    if (n_tiles == 1) {
+        fixup(0, lv0);
+        pf_barrier();
+    }
+    for (uint32_t t = 0; t < n_tiles; t += 2) {
+        compute(t * pf_bk, lk0, lv0);
+        if (t + 1 >= n_tiles) {
+            break;
+        }
+        pf_barrier();
+        if (t + 2 < n_tiles) {
+            issue((t + 2) * pf_bk, lk0, lv0);
+        }
+        wait_tile(t + 2 < n_tiles);
+        pf_barrier();
+        if (t + 2 == n_tiles) {
+            fixup((t + 1) * pf_bk, lv1);
+            pf_barrier();
+        }
+        compute((t + 1) * pf_bk, lk1, lv1);
+        if (t + 2 >= n_tiles) {
+            break;
+        }
+        pf_barrier();
+        if (t + 3 < n_tiles) {
+            issue((t + 3) * pf_bk, lk1, lv1);
+        }
+        wait_tile(t + 3 < n_tiles);
+        pf_barrier();
+        if (t + 3 == n_tiles) {
+            fixup((t + 2) * pf_bk, lv0);
+            pf_barrier();
+        }
+    }
+
+    if (my_q >= a.n) {
+        return;
+    }
+    const float inv = 1.0f / l_run;
+    float* out = a.out + static_cast<std::size_t>(my_q) * a.q_row + h * hd;
+    // Register i of tile n holds dim 32n + 8(i/4) + 4H + i%4.
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t d = 32 * n + 8 * b + 4 * H;
+            if (d < hd) {
+                *reinterpret_cast<f4*>(out + d) =
+                    f4{o[n][4 * b] * inv, o[n][4 * b + 1] * inv, o[n][4 * b + 2] * inv, o[n][4 * b + 3] * inv};
+            }
+        }
+    }
+}
+
+template <int HD>
+hipError_t launch_hd(const flash_args& a, uint32_t dtype, hipStream_t stream) {
+    const dim3 grid(a.n_heads * ((a.n + pf_bq - 1) / pf_bq));
+    if (dtype == 1) {
+        prefill_kernel<HD, true><<<grid, 256, 0, stream>>>(a);
+    } else {
+        prefill_kernel<HD, false><<<grid, 256, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool prefill_fits(uint32_t kv_len, uint32_t row, uint32_t hd, uint32_t ctx_stride) {
+    return uint64_t{kv_len} * row * 2 < (uint64_t{1} << 31) && uint64_t{hd} * ctx_stride * 2 < (uint64_t{1} << 31);
+}
+
+hipError_t launch_prefill(const flash_args& a, uint32_t q_dtype, hipStream_t stream) {
+    switch ((a.hd + 31) / 32 * 32) {
+    case 32:
+        return launch_hd<32>(a, q_dtype, stream);
+    case 64:
+        return launch_hd<64>(a, q_dtype, stream);
+    case 96:
+        return launch_hd<96>(a, q_dtype, stream);
+    case 128:
+        return launch_hd<128>(a, q_dtype, stream);
+    case 160:
+        return launch_hd<160>(a, q_dtype, stream);
+    case 192:
+        return launch_hd<192>(a, q_dtype, stream);
+    case 224:
+        return launch_hd<224>(a, q_dtype, stream);
+    case 256:
+        return launch_hd<256>(a, q_dtype, stream);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace syn

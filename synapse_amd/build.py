@@ -62,7 +62,9 @@ def build_library() -> pathlib.Path:
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(HIP_SOURCES))) as ex:
         objs = list(ex.map(compile_one, HIP_SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    # -z defs: an unresolved symbol fails the link (a kernel whose host stub
+    # the compiler silently dropped would otherwise surface only at load time).
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
     return LIB
 

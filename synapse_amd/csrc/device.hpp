@@ -67,6 +67,13 @@ __device__ __forceinline__ _Float16 to_h(float x) {
     return static_cast<_Float16>(x);
 }
 
+// acc + x.x + x.y in f32 (v_dot2_f32_f16 against (1, 1)): sums binary16
+// pairs with no conversions.
+__device__ __forceinline__ float add_pair(h2 x, float acc) {
+    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(fp16x2, x), __builtin_bit_cast(fp16x2, h2{1, 1}), acc, false);
+}
+
 // D(16x16) += A(16x32) B(32x16), f16 operands, f32 accumulate. Lane l holds
 // A[l%16][k-group l/16], B[k-group l/16][l%16] (8 k values each) and
 // D[4*(l/16) + i][l%16], i = 0..3.

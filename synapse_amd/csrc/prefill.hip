@@ -49,6 +49,12 @@ __device__ __forceinline__ void pf_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// One 1 KB tile copy: lane l's 16 bytes at byte `offset` of r land at
+// lds + 16 l (offsets at or past r's limit land as zeros).
+__device__ __forceinline__ void pf_copy(rsrc r, char* lds, uint32_t offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, offset, 0, 0, 0);
+}
+
 template <bool F16>
 __device__ __forceinline__ h8 pf_load_q(const void* base, std::size_t index) {
     if constexpr (F16) {
@@ -118,32 +124,54 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
     }
 
     // Tile copies, global -> LDS through buffer resources, 1 KB per wave
-    // instruction (buffer_load ... lds writes lane l's 16 bytes at +16 l):
-    // keys at or past kv_end and dims past hd arrive as zeros. LDS rows carry
-    // one 16-byte chunk of padding (K: 64 rows of KCPR + 1 chunks; V^T: HD rows
-    // of 8 + 1), so the operand reads below spread over the banks; a lane whose
-    // slot is padding, or slack past the V^T rows, copies an out-of-range zero.
-    // Copy j of a tile goes to wave j % 4.
-    const rsrc k_res = make_rsrc(a.k + g * hd, kv_end * a.row * 2 - g * hd * 2);
-    const rsrc v_res = make_rsrc(a.vt + static_cast<std::size_t>(g) * hd * a.ctx_stride, hd * a.ctx_stride * 2);
-    const auto issue = [&](uint32_t t0, char* sk, char* sv) {
+    // instruction (buffer_load ... lds writes lane l's 16 bytes at +16 l).
+    // LDS rows carry one 16-byte chunk of padding (K: 64 rows of KCPR + 1
+    // chunks; V^T: HD rows of 8 + 1), so the operand reads below spread over
+    // the banks. Copy j of a tile goes to wave j % 4. A lane's byte offset
+    // inside a tile is fixed, so it is computed once; the tile moves the
+    // resource base. Padding slots, dims past hd and slack past the V^T rows
+    // take an out-of-range offset and arrive as zeros; so do K rows at or past
+    // kv_end (the K resource ends there) and, in the last tile, V^T chunks
+    // that start at or past it.
+    constexpr int CPW = (TT + 3) / 4;  // copies per wave and tile, at most
+    uint32_t coff[CPW];
 #pragma unroll
-        for (int i = 0; i < (TT + 3) / 4; ++i) {
+    for (int i = 0; i < CPW; ++i) {
+        const uint32_t j = w + 4 * i;
+        coff[i] = buffer_oob;
+        if (j < TK) {
+            const uint32_t L = 64 * j + ln;
+            const uint32_t r = L / KROWC, cc = L % KROWC;
+            if (cc < KCPR && 8 * cc < hd) {
+                coff[i] = r * a.row * 2 + cc * 16;
+            }
+        } else if (j < TT) {
+            const uint32_t L = 64 * (j - TK) + ln;
+            const uint32_t d = L / VROWC, cc = L % VROWC;
+            if (cc < 8 && d < hd) {
+                coff[i] = d * a.ctx_stride * 2 + cc * 16;
+            }
+        }
+    }
+    const _Float16* k_head = a.k + g * hd;
+    const _Float16* v_head = a.vt + static_cast<std::size_t>(g) * hd * a.ctx_stride;
+    const uint32_t k_bytes = kv_end * a.row * 2 - g * hd * 2;  // through K row kv_end - 1 of head g
+    const uint32_t v_bytes = hd * a.ctx_stride * 2;
+    const auto issue = [&](uint32_t t0, char* sk, char* sv) {
+        const rsrc k_res = make_rsrc(k_head + static_cast<std::size_t>(t0) * a.row, k_bytes - t0 * a.row * 2);
+        const rsrc v_res = make_rsrc(v_head + t0, v_bytes - t0 * 2);
+        const bool last = t0 + pf_bk > kv_end;
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
             const uint32_t j = w + 4 * i;
             if (j < TK) {
-                const uint32_t L = 64 * j + ln;
-                const uint32_t r = L / KROWC, cc = L % KROWC;
-                const uint32_t key = t0 + r;
-                const uint32_t off = key < kv_end && cc < KCPR && 8 * cc < hd ? key * a.row * 2 + cc * 16 : buffer_oob;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    k_res, (__attribute__((address_space(3))) void*)(sk + 1024 * j), 16, off, 0, 0, 0);
+                pf_copy(k_res, sk + 1024 * j, coff[i]);
             } else if (j < TT) {
-                const uint32_t L = 64 * (j - TK) + ln;
-                const uint32_t d = L / VROWC, cc = L % VROWC;
-                const uint32_t key = t0 + 8 * cc;
-                const uint32_t off = key < kv_end && cc < 8 && d < hd ? d * a.ctx_stride * 2 + key * 2 : buffer_oob;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    v_res, (__attribute__((address_space(3))) void*)(sv + 1024 * (j - TK)), 16, off, 0, 0, 0);
+                uint32_t off = coff[i];
+                if (last && 8 * ((64 * (j - TK) + ln) % VROWC) >= kv_end - t0) {
+                    off = buffer_oob;
+                }
+                pf_copy(v_res, sv + 1024 * (j - TK), off);
             }
         }
     };
@@ -166,11 +194,15 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
             o[n][i] = 0.0f;
         }
     }
+    // Running max (raw q.k units) and sum of this lane's query. The max moves
+    // lazily: only when some query of the wave sees scores more than
+    // 8 / c above it (exp2 argument > 8), so most tiles skip the rescale of O;
+    // probabilities then stay <= 2^8, and O and the sum share the same max,
+    // so the quotient is unchanged.
     float m_run = -INFINITY, l_run = 0.0f;
 
     // One 64-key tile from one LDS stage.
     const auto compute = [&](uint32_t t0, const char* sk, const char* sv) {
-        __builtin_amdgcn_sched_barrier(0);
         if (q_row0 >= a.n || t0 > wave_last_pos) {
             return;  // every key of the tile is after every query of this wave
         }
@@ -188,46 +220,61 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
             }
         }
         // Register i of slice e holds key t0 + 32e + 16(i/8) + 8H + i%8.
+        if (t0 + pf_bk - 1 > a.pos + q_row0 || t0 + pf_bk > kv_end) {  // the tile crosses the diagonal or the end
+            const uint32_t lim = max(min(my_pos + 1, kv_end), t0) - t0;  // keys t0 + [0, lim) are visible
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t kk = 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
+                    sc[e][i] = kk < lim ? sc[e][i] : -INFINITY;
+                }
+            }
+        }
         float tmax = -INFINITY;
-        const bool diagonal = t0 + pf_bk - 1 > a.pos + q_row0 || t0 + pf_bk > kv_end;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                if (diagonal) {
-                    const uint32_t key = t0 + 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
-                    if (key > my_pos || key >= kv_end) {
-                        sc[e][i] = -INFINITY;
-                    }
-                }
                 tmax = fmaxf(tmax, sc[e][i]);
             }
         }
         tmax = max32(tmax);
-        const float m_new = fmaxf(m_run, tmax);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = fast_exp2((m_run - m_use) * c);
-        m_run = m_new;
+        // (both -inf: NaN, no growth; m_run -inf and tmax finite: +inf, growth.)
+        // The decision is the lane's own, so a query's result never depends
+        // on other queries' scores; the wave skips the work when no lane grows.
+        const bool grow = (tmax - m_run) * c > 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = grow ? tmax : m_run;
+            const float alpha = grow ? fast_exp2((m_run - m_new) * c) : 1.0f;
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    o[n][i] *= alpha;
+                }
+            }
+        }
+        const float mc = (m_run == -INFINITY ? 0.0f : m_run) * c;
         h8 pv[4];  // P^T operands: 16-key steps 0..3 of the tile
-        float psum = 0.0f;
-        const float mc = m_use * c;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const _Float16 ph = to_h(fast_exp2(sc[e][i] * c - mc));
-                pv[2 * e + (i >> 3)][i & 7] = ph;
-                psum += static_cast<float>(ph);
+                pv[2 * e + (i >> 3)][i & 7] = to_h(fast_exp2(sc[e][i] * c - mc));
             }
         }
-        l_run = l_run * alpha + sum32(psum);
+        float psum = 0.0f;
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
+        for (int s2 = 0; s2 < 4; ++s2) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                o[n][i] *= alpha;
+            for (int i = 0; i < 8; i += 2) {
+                psum = add_pair(h2{pv[s2][i], pv[s2][i + 1]}, psum);
             }
         }
+        l_run += sum32(psum);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
             const char* vrow = sv + ((32 * n + qi) * VROWC + H) * 16;  // V^T row 32n + qi, keys 8H..
@@ -236,7 +283,6 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
                 o[n] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[n]);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
     };
 
     // Pipeline over tiles, two stages: tile t computes from one stage while

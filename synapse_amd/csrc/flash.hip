@@ -18,7 +18,7 @@
 // multiply before exp2. Operands and P are binary16 for the matrix cores
 // (the reference keeps f32 here; the difference is within the parity bound).
 
-#include "kernels.hpp"
+#include "softmax.hpp"
 
 namespace syn {
 
@@ -232,6 +232,223 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
     }
 }
 
+// ---- head-resident form -------------------------------------------------------
+// When an image's K and V^T for one head fit in LDS (short rows, as a ViT's
+// 257 tokens), a block owns one (image, head): it stages all n keys once --
+// K rows padded by one 16-byte chunk, V transposed to V^T rows -- and then
+// its waves sweep their 32-query tiles over the resident keys in 32-key
+// slices, with no further barriers or global loads besides q. Keys past n
+// are zero rows and masked.
+
+// LDS bytes of the resident form for n keys (keys padded to a multiple of 32).
+__host__ __device__ constexpr uint32_t resident_lds_bytes(uint32_t n, uint32_t hdp) {
+    const uint32_t np = (n + 31) / 32 * 32;
+    return np * (hdp / 8 + 1) * 16 + hdp * (np / 8 + 1) * 16;
+}
+// Two blocks per CU: at most 80 KB each.
+constexpr uint32_t resident_lds_limit = 80 * 1024;
+// The most keys (a multiple of 32) the resident form holds at head size hdp.
+__host__ __device__ constexpr uint32_t resident_max_keys(uint32_t hdp) {
+    uint32_t np = 32;
+    while (resident_lds_bytes(np + 32, hdp) <= resident_lds_limit) {
+        np += 32;
+    }
+    return np;
+}
+
+template <int HD, bool F16>
+__global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
+    constexpr int NS = HD / 16;      // k-steps of the score product
+    constexpr int NT = HD / 32;      // 32-dim tiles of the output
+    constexpr int KCPR = HD / 8;     // 16-byte chunks of a K row
+    constexpr int KROWC = KCPR + 1;  // LDS K row in chunks (one of padding)
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ln = tid & 63;
+    const int H = ln >> 5;
+    const int qi = ln & 31;
+    const uint32_t n = a.n;
+    const uint32_t hd = a.hd;
+    const uint32_t np = (n + 31) / 32 * 32;
+    const uint32_t vrowc = np / 8 + 1;  // LDS V^T row in chunks (one of padding)
+    const uint32_t h = blockIdx.x % a.n_heads;
+    const uint32_t img = blockIdx.x / a.n_heads;
+    const std::size_t row_base = static_cast<std::size_t>(img) * n;
+    const float c = a.scale_log2e;
+    char* lk = lds;
+    char* lv = lds + np * KROWC * 16;
+
+    // ---- stage K rows and V^T (zeros past n and past hd) ----
+    // Every load of the block is issued before any LDS write, so staging
+    // costs one memory latency: CH chunks per thread at most (the largest n
+    // the resident form takes for this head size).
+    constexpr uint32_t CH = (resident_max_keys(HD) * KCPR + 255) / 256;
+    constexpr uint32_t ESZ = F16 ? 2 : 4;
+    const uint32_t nchunks = np * KCPR;
+    // The image's rows through buffer resources: chunks past n or past hd
+    // take an out-of-range offset and read as zeros, so every load is
+    // unconditional.
+    const uint32_t img_bytes = n * a.row * ESZ;
+    const rsrc k_res = make_rsrc(static_cast<const char*>(a.k_rows) + row_base * a.row * ESZ, img_bytes);
+    const rsrc v_res = make_rsrc(static_cast<const char*>(a.v_rows) + row_base * a.row * ESZ, img_bytes);
+    const auto chunk = [&](rsrc r, uint32_t off) {
+        if constexpr (F16) {
+            return buffer_load16(r, off);
+        } else {
+            const f4 lo = __builtin_bit_cast(f4, buffer_load16(r, off));
+            const f4 hi = __builtin_bit_cast(f4, buffer_load16(r, off == buffer_oob ? off : off + 16));
+            return as_u4(h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]), to_h(hi[0]), to_h(hi[1]),
+                            to_h(hi[2]), to_h(hi[3])});
+        }
+    };
+    // The wave's q tiles (wave (w + block) % 4 takes tiles w', w' + 4, ..., so
+    // the extra tiles of co-resident blocks land on different SIMDs) are
+    // loaded first, with the block's K and V: one memory latency for all.
+    constexpr uint32_t TPW = (resident_max_keys(HD) / 32 + 3) / 4;  // q tiles per wave, at most
+    const uint32_t n_qt = np / 32;
+    const uint32_t w0 = (static_cast<uint32_t>(w) + blockIdx.x) % 4;
+    const rsrc q_res = make_rsrc(static_cast<const char*>(a.q) + row_base * a.q_row * ESZ, n * a.q_row * ESZ);
+    u4 qc[TPW][NS];
+#pragma unroll
+    for (uint32_t t = 0; t < TPW; ++t) {
+        const uint32_t my_q = 32 * (w0 + 4 * t) + qi;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const uint32_t d0 = H * (HD / 2) + 8 * st;
+            qc[t][st] = chunk(q_res, my_q < n && d0 < hd ? (my_q * a.q_row + h * hd + d0) * ESZ : buffer_oob);
+        }
+    }
+    u4 kc[CH], vc[CH];
+#pragma unroll
+    for (uint32_t i = 0; i < CH; ++i) {
+        const uint32_t idx = tid + 256 * i;
+        const uint32_t key = idx / KCPR, cc = idx % KCPR;
+        kc[i] = chunk(k_res, idx < nchunks && key < n && 8 * cc < hd ? (key * a.row + h * hd + 8 * cc) * ESZ
+                                                                      : buffer_oob);
+        // V: lanes take consecutive keys of one 8-dim chunk, so each of the
+        // 8 half-word writes of a wave covers 128 contiguous bytes of a V^T row.
+        const uint32_t vkey = idx % np, vcc = idx / np;
+        vc[i] = chunk(v_res, idx < nchunks && vkey < n && 8 * vcc < hd ? (vkey * a.row + h * hd + 8 * vcc) * ESZ
+                                                                         : buffer_oob);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < CH; ++i) {
+        const uint32_t idx = tid + 256 * i;
+        if (idx < nchunks) {
+            const uint32_t key = idx / KCPR, cc = idx % KCPR;
+            *reinterpret_cast<u4*>(lk + (key * KROWC + cc) * 16) = kc[i];
+            const uint32_t vkey = idx % np, vcc = idx / np;
+            const h8 hv = as_h8(vc[i]);
+            _Float16* col = reinterpret_cast<_Float16*>(lv) + (8 * vcc * vrowc * 8 + vkey);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                col[j * vrowc * 8] = hv[j];
+            }
+        }
+    }
+    // The V^T padding chunks are never read; the K padding chunk neither.
+    __syncthreads();
+
+    // ---- the wave's query tiles over the resident keys ----
+#pragma unroll
+    for (uint32_t tq = 0; tq < TPW; ++tq) {
+        const uint32_t qt = w0 + 4 * tq;
+        if (qt >= n_qt) {
+            break;
+        }
+        const uint32_t my_q = 32 * qt + qi;
+        h8 qv[NS];
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            qv[st] = as_h8(qc[tq][st]);
+        }
+        f16v o[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                o[t][i] = 0.0f;
+            }
+        }
+        float m_run = -INFINITY, l_run = 0.0f;
+        // E 32-key slices from key t0 (keys past n masked).
+        const auto step = [&]<int E>(uint32_t t0) __attribute__((always_inline)) {
+            f16v sc[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    sc[e][i] = 0.0f;
+                }
+                const char* krow = lk + ((t0 + 32 * e + slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
+#pragma unroll
+                for (int st = 0; st < NS; ++st) {
+                    sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
+                }
+            }
+            // Register i of slice e holds key t0 + 32e + 16(i/8) + 8H + i%8.
+            if (t0 + 32 * E > n) {
+                const uint32_t lim = n - t0;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const uint32_t kk = 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
+                        sc[e][i] = kk < lim ? sc[e][i] : -INFINITY;
+                    }
+                }
+            }
+            h8 pv[2 * E];
+            online_softmax<E, NT>(sc, c, m_run, l_run, o, pv);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                // V^T row 32t + qi, keys t0 + 8H + 16 s ..
+                const char* vrow = lv + ((32 * t + qi) * vrowc + t0 / 8 + H) * 16;
+#pragma unroll
+                for (int s2 = 0; s2 < 2 * E; ++s2) {
+                    o[t] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[t]);
+                }
+            }
+        };
+        uint32_t t0 = 0;
+        for (; t0 + 64 <= np; t0 += 64) {
+            step.template operator()<2>(t0);
+        }
+        if (t0 < np) {
+            step.template operator()<1>(t0);
+        }
+        if (my_q < n) {
+            const float inv = 1.0f / l_run;
+            float* out = a.out + (row_base + my_q) * a.q_row + h * hd;
+            // Register i of tile t holds dim 32t + 8(i/4) + 4H + i%4.
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t d = 32 * t + 8 * b + 4 * H;
+                    if (d < hd) {
+                        *reinterpret_cast<f4*>(out + d) = f4{o[t][4 * b] * inv, o[t][4 * b + 1] * inv,
+                                                             o[t][4 * b + 2] * inv, o[t][4 * b + 3] * inv};
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int HD>
+hipError_t launch_resident(const flash_args& a, uint32_t dtype, uint32_t lds_bytes, hipStream_t stream) {
+    const dim3 grid(a.n_heads * a.batch);
+    if (dtype == 1) {
+        resident_kernel<HD, true><<<grid, 256, lds_bytes, stream>>>(a);
+    } else {
+        resident_kernel<HD, false><<<grid, 256, lds_bytes, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
 template <int HD>
 hipError_t launch_hd(const flash_args& a, uint32_t dtype, hipStream_t stream) {
     const dim3 grid((a.n + bq - 1) / bq, a.n_heads, a.batch);
@@ -246,7 +463,26 @@ hipError_t launch_hd(const flash_args& a, uint32_t dtype, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream) {
-    switch ((a.hd + 31) / 32 * 32) {
+    const uint32_t hdp = (a.hd + 31) / 32 * 32;
+    // Resident form while two blocks fit a CU's LDS (160 KB).
+    // (An image's rows are addressed through one buffer resource: < 2^31 bytes.)
+    if (hdp <= 128 && uint64_t{a.n_heads} * a.batch <= 0x7fffffffu &&
+        uint64_t{a.n} * a.row * (in_dtype == 1 ? 2 : 4) < (uint64_t{1} << 31)) {
+        const uint32_t bytes = resident_lds_bytes(a.n, hdp);
+        if (bytes <= resident_lds_limit) {
+            switch (hdp) {
+            case 32:
+                return launch_resident<32>(a, in_dtype, bytes, stream);
+            case 64:
+                return launch_resident<64>(a, in_dtype, bytes, stream);
+            case 96:
+                return launch_resident<96>(a, in_dtype, bytes, stream);
+            default:
+                return launch_resident<128>(a, in_dtype, bytes, stream);
+            }
+        }
+    }
+    switch (hdp) {
     case 32:
         return launch_hd<32>(a, in_dtype, stream);
     case 64:

@@ -45,12 +45,21 @@ def test_vision_clip_vit_l14(arena):
     _vision(arena, c.n, c.batch, c.n_heads, c.head_dim, SYN_F16, c.sigma, seed=wl.SEED, images=[0, 7, 20, 31])
 
 
-@pytest.mark.parametrize("n,hd", [(37, 8), (1, 8), (6, 16), (50, 24), (130, 64), (257, 128), (64, 256)])
+@pytest.mark.parametrize("n,hd", [(37, 8), (1, 8), (6, 16), (50, 24), (130, 64), (257, 128), (64, 256),
+                                  (288, 64), (289, 64), (577, 64), (128, 128), (129, 128), (31, 96)])
 def test_vision_shapes_f32_inputs(arena, n, hd):
     """The reference's self-attention cases (tests/sdk/kernels_vision.cpp:
     200-250, n in {37, 1, 6, 13, 50}) with f32 inputs, which the kernel
-    rounds to binary16 for the matrix cores."""
+    rounds to binary16 for the matrix cores. The shapes cover both forms:
+    keys resident in LDS (n up to 288 at hd 64, 128 at hd 128) and tiled."""
     _vision(arena, n, 2, 3, hd, SYN_F32)
+
+
+@pytest.mark.parametrize("n,hd", [(257, 64), (577, 64), (100, 128)])
+def test_vision_many_heads_f16(arena, n, hd):
+    """Several images and heads at once with f16 inputs: every (image, head)
+    block of the grid is checked."""
+    _vision(arena, n, 3, 5, hd, SYN_F16, seed=11)
 
 
 @pytest.mark.parametrize("n,hd", [(13, 12), (50, 20), (6, 4)])

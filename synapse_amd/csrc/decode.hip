@@ -198,9 +198,12 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     // rounded to binary16 as attend_group rounds q (S/kernels/attention.hpp:204-206).
     h8 qv[NS];
     const auto convert_q = [&]() {
-        // Wait for q's copy only: the K, V loads issued after it stay in flight.
+        // Wait for q's copy only: the K, V loads issued after it stay in
+        // flight. Every wave has waited for its own copies, so the barrier
+        // needs no more than the LDS counter (__syncthreads() would also wait
+        // for the K, V loads).
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NS + NT));
-        __syncthreads();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             const uint32_t d0 = G * SPAN + 8 * st;

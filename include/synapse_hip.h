@@ -196,6 +196,70 @@ typedef struct syn_rope_desc {
 
 int syn_hip_rope(syn_arena* arena, const syn_rope_desc* desc);
 
+/* ---- the rest of a Llama-family decode graph ---------------------------------
+ * With syn_hip_rope and syn_hip_attention these run a whole layer stack from
+ * one arena (all rows f32). */
+
+/* Embedding rows: out row i = table row tokens[i] (tokens from host memory,
+ * each checked < n_table_rows). Replaces session::execute(const op_embed&),
+ * S/graph/session.hpp:331-336. */
+typedef struct syn_embed_desc {
+    uint64_t table_offset; /* n_table_rows rows of size f32 */
+    uint64_t out_offset;   /* n rows of size f32 */
+    uint32_t n_table_rows;
+    uint32_t size;
+} syn_embed_desc;
+
+int syn_hip_embed(syn_arena* arena, const syn_embed_desc* desc, const uint32_t* tokens, uint32_t n);
+
+/* RMSNorm per row: out = (x * (1 / sqrt(mean(x^2) + eps))) * gamma, squares
+ * summed in double. Replaces execute(const op_rms_norm&), :324-330
+ * (kernels::rms_norm, S/kernels/elementwise.hpp:208-235). */
+typedef struct syn_norm_desc {
+    uint64_t in_offset;     /* n rows of size f32 */
+    uint64_t weight_offset; /* size f32 (gamma) */
+    uint64_t out_offset;    /* n rows of size f32; may alias in */
+    uint32_t n;
+    uint32_t size;
+    float eps;              /* > 0 */
+    uint32_t reserved;
+} syn_norm_desc;
+
+int syn_hip_rms_norm(syn_arena* arena, const syn_norm_desc* desc);
+
+/* F32 matrix product: out[r][o] = sum_c w[o][c] x[r][c] (+ bias[o]).
+ * Replaces execute(const op_matmul&) for F32 weights, :287-302, and
+ * execute(const op_add_bias&), :306-312. */
+typedef struct syn_matmul_desc {
+    uint64_t w_offset;    /* rows x cols f32, row-major (GGUF ne = {cols, rows}) */
+    uint64_t x_offset;    /* n rows of cols f32 */
+    uint64_t bias_offset; /* rows f32, or UINT64_MAX for none */
+    uint64_t out_offset;  /* n rows of rows f32; may not alias x */
+    uint32_t n;
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t reserved;
+} syn_matmul_desc;
+
+int syn_hip_matmul(syn_arena* arena, const syn_matmul_desc* desc);
+
+/* Element-wise over count floats (S/kernels/elementwise.hpp:28-81):
+ * SYN_ADD a + b (op_add), SYN_MUL a * b (op_mul), SYN_SILU_MUL silu(a) * b
+ * (op_silu then op_mul), SYN_SCALE a * scalar (kernels::scale, as
+ * op_attn_temperature applies it). out may alias a or b. */
+enum { SYN_ADD = 0, SYN_MUL = 1, SYN_SILU_MUL = 2, SYN_SCALE = 3 };
+
+typedef struct syn_elementwise_desc {
+    uint64_t a_offset;
+    uint64_t b_offset;   /* unused by SYN_SCALE */
+    uint64_t out_offset;
+    uint64_t count;
+    uint32_t op;
+    float scalar;
+} syn_elementwise_desc;
+
+int syn_hip_elementwise(syn_arena* arena, const syn_elementwise_desc* desc);
+
 #ifdef __cplusplus
 }
 #endif

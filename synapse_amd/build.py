@@ -39,7 +39,8 @@ HIP_FLAGS = [
     # Packed-FP32 instructions stay off on this pool (wrong results seen).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-HIP_SOURCES = ["kv_append.hip", "decode.hip", "prefill.hip", "flash.hip", "generic.hip", "rope.hip", "capi.hip"]
+HIP_SOURCES = ["kv_append.hip", "decode.hip", "prefill.hip", "flash.hip", "generic.hip", "rope.hip", "ops.hip",
+               "capi.hip"]
 
 
 def _run(cmd: list[str], cwd: pathlib.Path | None = None) -> None:

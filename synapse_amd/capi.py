@@ -47,6 +47,28 @@ class RopeDesc(ctypes.Structure):
                 ("ext_factor", f32), ("attn_factor", f32), ("corr_low", f32), ("corr_high", f32)]
 
 
+class EmbedDesc(ctypes.Structure):
+    _fields_ = [("table_offset", u64), ("out_offset", u64), ("n_table_rows", u32), ("size", u32)]
+
+
+class NormDesc(ctypes.Structure):
+    _fields_ = [("in_offset", u64), ("weight_offset", u64), ("out_offset", u64), ("n", u32), ("size", u32),
+                ("eps", f32), ("reserved", u32)]
+
+
+class MatmulDesc(ctypes.Structure):
+    _fields_ = [("w_offset", u64), ("x_offset", u64), ("bias_offset", u64), ("out_offset", u64), ("n", u32),
+                ("rows", u32), ("cols", u32), ("reserved", u32)]
+
+
+class ElementwiseDesc(ctypes.Structure):
+    _fields_ = [("a_offset", u64), ("b_offset", u64), ("out_offset", u64), ("count", u64), ("op", u32),
+                ("scalar", f32)]
+
+
+SYN_ADD, SYN_MUL, SYN_SILU_MUL, SYN_SCALE = 0, 1, 2, 3
+
+
 # name -> (restype, argtypes); every symbol include/synapse_hip.h declares.
 SIGNATURES = {
     "syn_hip_error_string": (ctypes.c_char_p, [i32]),
@@ -70,6 +92,10 @@ SIGNATURES = {
     "syn_hip_attend_batch": (i32, [ctypes.c_void_p, ctypes.POINTER(SeqDesc), u32, u32, f32, u32, u64, u64]),
     "syn_hip_self_attention": (i32, [ctypes.c_void_p, ctypes.POINTER(SelfDesc)]),
     "syn_hip_rope": (i32, [ctypes.c_void_p, ctypes.POINTER(RopeDesc)]),
+    "syn_hip_embed": (i32, [ctypes.c_void_p, ctypes.POINTER(EmbedDesc), ctypes.POINTER(u32), u32]),
+    "syn_hip_rms_norm": (i32, [ctypes.c_void_p, ctypes.POINTER(NormDesc)]),
+    "syn_hip_matmul": (i32, [ctypes.c_void_p, ctypes.POINTER(MatmulDesc)]),
+    "syn_hip_elementwise": (i32, [ctypes.c_void_p, ctypes.POINTER(ElementwiseDesc)]),
 }
 
 _lib = None

@@ -726,4 +726,149 @@ int syn_hip_rope(syn_arena* a, const syn_rope_desc* d) {
     return hip_status(syn::launch_rope(r, a->stream), "rope launch");
 }
 
+int syn_hip_embed(syn_arena* a, const syn_embed_desc* d, const uint32_t* tokens, uint32_t n) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr || (tokens == nullptr && n > 0)) {
+        return fail(SYN_HIP_EINVAL, "null descriptor or tokens");
+    }
+    if (d->size == 0 || d->n_table_rows == 0) {
+        return fail(SYN_HIP_EINVAL, "embed: %u rows of size %u", d->n_table_rows, d->size);
+    }
+    if (n == 0) {
+        return SYN_HIP_OK;
+    }
+    if (int e = check_range(a, d->table_offset, uint64_t{d->n_table_rows} * d->size * 4, 4, "embed table")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, uint64_t{n} * d->size * 4, 4, "embed out")) {
+        return e;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (tokens[i] >= d->n_table_rows) {
+            return fail(SYN_HIP_EINVAL, "embed: token %u at %u, table has %u rows", tokens[i], i, d->n_table_rows);
+        }
+    }
+    const auto* table = reinterpret_cast<const float*>(a->base + d->table_offset);
+    auto* out = reinterpret_cast<float*>(a->base + d->out_offset);
+    for (uint32_t i0 = 0; i0 < n; i0 += syn::embed_max_tokens) {
+        const uint32_t m = std::min(n - i0, syn::embed_max_tokens);
+        syn::embed_tokens t{};
+        std::copy(tokens + i0, tokens + i0 + m, t.token);
+        if (int e = hip_status(syn::launch_embed(table, out + uint64_t{i0} * d->size, t, m, d->size, a->stream),
+                               "embed launch")) {
+            return e;
+        }
+    }
+    return SYN_HIP_OK;
+}
+
+int syn_hip_rms_norm(syn_arena* a, const syn_norm_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->size == 0 || !(std::isfinite(d->eps) && d->eps > 0.0f)) {
+        return fail(SYN_HIP_EINVAL, "rms_norm: size %u, eps %g", d->size, static_cast<double>(d->eps));
+    }
+    if (d->n == 0) {
+        return SYN_HIP_OK;
+    }
+    const uint64_t bytes = uint64_t{d->n} * d->size * 4;
+    if (int e = check_range(a, d->in_offset, bytes, 4, "rms_norm in")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, bytes, 4, "rms_norm out")) {
+        return e;
+    }
+    if (int e = check_range(a, d->weight_offset, uint64_t{d->size} * 4, 4, "rms_norm weight")) {
+        return e;
+    }
+    return hip_status(syn::launch_rms_norm(reinterpret_cast<const float*>(a->base + d->in_offset),
+                                           reinterpret_cast<const float*>(a->base + d->weight_offset),
+                                           reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->size, d->eps,
+                                           a->stream),
+                      "rms_norm launch");
+}
+
+int syn_hip_matmul(syn_arena* a, const syn_matmul_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->rows == 0 || d->cols == 0 || d->n > 65535) {
+        return fail(SYN_HIP_EINVAL, "matmul: %u x %u weights, %u rows", d->rows, d->cols, d->n);
+    }
+    if (d->n == 0) {
+        return SYN_HIP_OK;
+    }
+    const uint64_t x_bytes = uint64_t{d->n} * d->cols * 4;
+    const uint64_t out_bytes = uint64_t{d->n} * d->rows * 4;
+    if (int e = check_range(a, d->w_offset, uint64_t{d->rows} * d->cols * 4, 4, "matmul w")) {
+        return e;
+    }
+    if (int e = check_range(a, d->x_offset, x_bytes, 4, "matmul x")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, out_bytes, 4, "matmul out")) {
+        return e;
+    }
+    if (d->x_offset < d->out_offset + out_bytes && d->out_offset < d->x_offset + x_bytes) {
+        return fail(SYN_HIP_EINVAL, "matmul: out aliases x");
+    }
+    const float* bias = nullptr;
+    if (d->bias_offset != no_offset) {
+        if (int e = check_range(a, d->bias_offset, uint64_t{d->rows} * 4, 4, "matmul bias")) {
+            return e;
+        }
+        bias = reinterpret_cast<const float*>(a->base + d->bias_offset);
+    }
+    return hip_status(syn::launch_matmul(reinterpret_cast<const float*>(a->base + d->w_offset),
+                                         reinterpret_cast<const float*>(a->base + d->x_offset), bias,
+                                         reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->rows, d->cols,
+                                         a->stream),
+                      "matmul launch");
+}
+
+int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->op > SYN_SCALE) {
+        return fail(SYN_HIP_EINVAL, "elementwise: op %u", d->op);
+    }
+    if (d->count == 0) {
+        return SYN_HIP_OK;
+    }
+    if (d->count > (uint64_t{1} << 40)) {
+        return fail(SYN_HIP_EINVAL, "elementwise: count %llu", static_cast<unsigned long long>(d->count));
+    }
+    const uint64_t bytes = d->count * 4;
+    if (int e = check_range(a, d->a_offset, bytes, 4, "elementwise a")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, bytes, 4, "elementwise out")) {
+        return e;
+    }
+    const float* b = nullptr;
+    if (d->op != SYN_SCALE) {
+        if (int e = check_range(a, d->b_offset, bytes, 4, "elementwise b")) {
+            return e;
+        }
+        b = reinterpret_cast<const float*>(a->base + d->b_offset);
+    }
+    return hip_status(syn::launch_elementwise(reinterpret_cast<const float*>(a->base + d->a_offset), b,
+                                              reinterpret_cast<float*>(a->base + d->out_offset), d->count, d->op,
+                                              d->scalar, a->stream),
+                      "elementwise launch");
+}
+
 }  // extern "C"

@@ -121,4 +121,24 @@ struct rope_args {
 };
 hipError_t launch_rope(const rope_args& a, hipStream_t stream);
 
+// ---- the rest of a decode graph (ops.hip) -----------------------------------
+constexpr uint32_t embed_max_tokens = 256;  // tokens per embed launch (kernel argument)
+struct embed_tokens {
+    uint32_t token[embed_max_tokens];
+};
+enum elementwise_op : uint32_t {
+    elementwise_add = 0,       // a + b
+    elementwise_mul = 1,       // a * b
+    elementwise_silu_mul = 2,  // silu(a) * b
+    elementwise_scale = 3,     // a * scalar
+};
+hipError_t launch_embed(const float* table, float* out, const embed_tokens& t, uint32_t n, uint32_t size,
+                        hipStream_t stream);
+hipError_t launch_rms_norm(const float* in, const float* gamma, float* out, uint32_t n, uint32_t size, float eps,
+                           hipStream_t stream);
+hipError_t launch_matmul(const float* w, const float* x, const float* bias, float* out, uint32_t n, uint32_t rows,
+                         uint32_t cols, hipStream_t stream);
+hipError_t launch_elementwise(const float* a, const float* b, float* out, uint64_t count, uint32_t op, float scalar,
+                              hipStream_t stream);
+
 }  // namespace syn

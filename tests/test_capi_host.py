@@ -47,7 +47,9 @@ def test_descriptor_layouts_match_the_header(tmp_path):
     if cc is None:
         pytest.skip("no host C compiler")
     structs = {"syn_kv_desc": capi.KvDesc, "syn_attn_desc": capi.AttnDesc, "syn_seq_desc": capi.SeqDesc,
-               "syn_self_desc": capi.SelfDesc, "syn_rope_desc": capi.RopeDesc}
+               "syn_self_desc": capi.SelfDesc, "syn_rope_desc": capi.RopeDesc, "syn_embed_desc": capi.EmbedDesc,
+               "syn_norm_desc": capi.NormDesc, "syn_matmul_desc": capi.MatmulDesc,
+               "syn_elementwise_desc": capi.ElementwiseDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, ct in structs.items():
         lines.append(f'printf("{cname} @sizeof %zu\\n", sizeof({cname}));')

@@ -243,11 +243,12 @@ typedef struct syn_matmul_desc {
 
 int syn_hip_matmul(syn_arena* arena, const syn_matmul_desc* desc);
 
-/* Element-wise over count floats (S/kernels/elementwise.hpp:28-81):
- * SYN_ADD a + b (op_add), SYN_MUL a * b (op_mul), SYN_SILU_MUL silu(a) * b
- * (op_silu then op_mul), SYN_SCALE a * scalar (kernels::scale, as
- * op_attn_temperature applies it). out may alias a or b. */
-enum { SYN_ADD = 0, SYN_MUL = 1, SYN_SILU_MUL = 2, SYN_SCALE = 3 };
+/* Element-wise over count floats (S/kernels/elementwise.hpp:28-81, :115-167):
+ * SYN_ADD a + b (op_add, and op_add_rows over whole tables), SYN_MUL a * b
+ * (op_mul), SYN_SILU_MUL silu(a) * b (op_silu then op_mul), SYN_SCALE
+ * a * scalar (kernels::scale, as op_attn_temperature applies it), SYN_GELU
+ * gelu(a) in ggml's binary16-rounded form (op_gelu). out may alias a or b. */
+enum { SYN_ADD = 0, SYN_MUL = 1, SYN_SILU_MUL = 2, SYN_SCALE = 3, SYN_GELU = 4 };
 
 typedef struct syn_elementwise_desc {
     uint64_t a_offset;
@@ -259,6 +260,37 @@ typedef struct syn_elementwise_desc {
 } syn_elementwise_desc;
 
 int syn_hip_elementwise(syn_arena* arena, const syn_elementwise_desc* desc);
+
+/* Layer norm per row: ((x - mean) / sqrt(var + eps)) * gamma + beta, sums in
+ * double. Replaces execute(const op_layer_norm&), S/graph/session.hpp:380-392
+ * (kernels::layer_norm, S/kernels/elementwise.hpp:240-305). */
+typedef struct syn_layer_norm_desc {
+    uint64_t in_offset;     /* n rows of size f32 */
+    uint64_t weight_offset; /* size f32 (gamma) */
+    uint64_t bias_offset;   /* size f32 (beta), or UINT64_MAX for none */
+    uint64_t out_offset;    /* n rows of size f32; may alias in */
+    uint32_t n;
+    uint32_t size;
+    float eps;              /* > 0 */
+    uint32_t reserved;
+} syn_layer_norm_desc;
+
+int syn_hip_layer_norm(syn_arena* arena, const syn_layer_norm_desc* desc);
+
+/* Pixel shuffle of a grid_w x grid_h grid of patch rows (n f32 each) into
+ * (grid_w/s)(grid_h/s) rows of s*s*n. Replaces execute(const
+ * op_pixel_shuffle&), :450-453 (kernels::pixel_shuffle,
+ * S/kernels/elementwise.hpp:307-333). */
+typedef struct syn_pixel_shuffle_desc {
+    uint64_t in_offset;
+    uint64_t out_offset; /* may not alias in */
+    uint32_t n;
+    uint32_t grid_w;
+    uint32_t grid_h;
+    uint32_t scale;      /* >= 1, divides grid_w and grid_h */
+} syn_pixel_shuffle_desc;
+
+int syn_hip_pixel_shuffle(syn_arena* arena, const syn_pixel_shuffle_desc* desc);
 
 #ifdef __cplusplus
 }

@@ -66,7 +66,17 @@ class ElementwiseDesc(ctypes.Structure):
                 ("scalar", f32)]
 
 
-SYN_ADD, SYN_MUL, SYN_SILU_MUL, SYN_SCALE = 0, 1, 2, 3
+class LayerNormDesc(ctypes.Structure):
+    _fields_ = [("in_offset", u64), ("weight_offset", u64), ("bias_offset", u64), ("out_offset", u64), ("n", u32),
+                ("size", u32), ("eps", f32), ("reserved", u32)]
+
+
+class PixelShuffleDesc(ctypes.Structure):
+    _fields_ = [("in_offset", u64), ("out_offset", u64), ("n", u32), ("grid_w", u32), ("grid_h", u32),
+                ("scale", u32)]
+
+
+SYN_ADD, SYN_MUL, SYN_SILU_MUL, SYN_SCALE, SYN_GELU = 0, 1, 2, 3, 4
 
 
 # name -> (restype, argtypes); every symbol include/synapse_hip.h declares.
@@ -96,6 +106,8 @@ SIGNATURES = {
     "syn_hip_rms_norm": (i32, [ctypes.c_void_p, ctypes.POINTER(NormDesc)]),
     "syn_hip_matmul": (i32, [ctypes.c_void_p, ctypes.POINTER(MatmulDesc)]),
     "syn_hip_elementwise": (i32, [ctypes.c_void_p, ctypes.POINTER(ElementwiseDesc)]),
+    "syn_hip_layer_norm": (i32, [ctypes.c_void_p, ctypes.POINTER(LayerNormDesc)]),
+    "syn_hip_pixel_shuffle": (i32, [ctypes.c_void_p, ctypes.POINTER(PixelShuffleDesc)]),
 }
 
 _lib = None

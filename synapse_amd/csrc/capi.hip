@@ -842,7 +842,7 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
     if (d == nullptr) {
         return fail(SYN_HIP_EINVAL, "null descriptor");
     }
-    if (d->op > SYN_SCALE) {
+    if (d->op > SYN_GELU) {
         return fail(SYN_HIP_EINVAL, "elementwise: op %u", d->op);
     }
     if (d->count == 0) {
@@ -859,7 +859,7 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
         return e;
     }
     const float* b = nullptr;
-    if (d->op != SYN_SCALE) {
+    if (d->op != SYN_SCALE && d->op != SYN_GELU) {
         if (int e = check_range(a, d->b_offset, bytes, 4, "elementwise b")) {
             return e;
         }
@@ -869,6 +869,71 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
                                               reinterpret_cast<float*>(a->base + d->out_offset), d->count, d->op,
                                               d->scalar, a->stream),
                       "elementwise launch");
+}
+
+int syn_hip_layer_norm(syn_arena* a, const syn_layer_norm_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->size == 0 || !(std::isfinite(d->eps) && d->eps > 0.0f)) {
+        return fail(SYN_HIP_EINVAL, "layer_norm: size %u, eps %g", d->size, static_cast<double>(d->eps));
+    }
+    if (d->n == 0) {
+        return SYN_HIP_OK;
+    }
+    const uint64_t bytes = uint64_t{d->n} * d->size * 4;
+    if (int e = check_range(a, d->in_offset, bytes, 4, "layer_norm in")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, bytes, 4, "layer_norm out")) {
+        return e;
+    }
+    if (int e = check_range(a, d->weight_offset, uint64_t{d->size} * 4, 4, "layer_norm weight")) {
+        return e;
+    }
+    const float* beta = nullptr;
+    if (d->bias_offset != no_offset) {
+        if (int e = check_range(a, d->bias_offset, uint64_t{d->size} * 4, 4, "layer_norm bias")) {
+            return e;
+        }
+        beta = reinterpret_cast<const float*>(a->base + d->bias_offset);
+    }
+    return hip_status(syn::launch_layer_norm(reinterpret_cast<const float*>(a->base + d->in_offset),
+                                             reinterpret_cast<const float*>(a->base + d->weight_offset), beta,
+                                             reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->size, d->eps,
+                                             a->stream),
+                      "layer_norm launch");
+}
+
+int syn_hip_pixel_shuffle(syn_arena* a, const syn_pixel_shuffle_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->n == 0 || d->scale == 0 || d->grid_w == 0 || d->grid_h == 0 || d->grid_w % d->scale != 0 ||
+        d->grid_h % d->scale != 0) {
+        return fail(SYN_HIP_EINVAL, "pixel_shuffle: %u x %u grid of %u, scale %u", d->grid_w, d->grid_h, d->n,
+                    d->scale);
+    }
+    const uint64_t bytes = uint64_t{d->grid_w} * d->grid_h * d->n * 4;
+    if (int e = check_range(a, d->in_offset, bytes, 4, "pixel_shuffle in")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, bytes, 4, "pixel_shuffle out")) {
+        return e;
+    }
+    if (d->in_offset < d->out_offset + bytes && d->out_offset < d->in_offset + bytes) {
+        return fail(SYN_HIP_EINVAL, "pixel_shuffle: out aliases in");
+    }
+    return hip_status(syn::launch_pixel_shuffle(reinterpret_cast<const float*>(a->base + d->in_offset),
+                                                reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->grid_w,
+                                                d->grid_h, d->scale, a->stream),
+                      "pixel_shuffle launch");
 }
 
 }  // extern "C"

@@ -131,6 +131,7 @@ enum elementwise_op : uint32_t {
     elementwise_mul = 1,       // a * b
     elementwise_silu_mul = 2,  // silu(a) * b
     elementwise_scale = 3,     // a * scalar
+    elementwise_gelu = 4,      // gelu(a), ggml's binary16-rounded tanh form
 };
 hipError_t launch_embed(const float* table, float* out, const embed_tokens& t, uint32_t n, uint32_t size,
                         hipStream_t stream);
@@ -140,5 +141,9 @@ hipError_t launch_matmul(const float* w, const float* x, const float* bias, floa
                          uint32_t cols, hipStream_t stream);
 hipError_t launch_elementwise(const float* a, const float* b, float* out, uint64_t count, uint32_t op, float scalar,
                               hipStream_t stream);
+hipError_t launch_layer_norm(const float* in, const float* gamma, const float* beta, float* out, uint32_t n,
+                             uint32_t size, float eps, hipStream_t stream);
+hipError_t launch_pixel_shuffle(const float* in, float* out, uint32_t n, uint32_t grid_w, uint32_t grid_h, uint32_t s,
+                                hipStream_t stream);
 
 }  // namespace syn

@@ -1,5 +1,6 @@
-// ops.hip — the rest of a Llama-family decode graph on the device: embedding
-// rows, RMSNorm, F32 matrix products, and the element-wise ops between them.
+// ops.hip — the rest of the reference's model graphs on the device: embedding
+// rows, RMSNorm and layer norm, F32 matrix products, the element-wise ops
+// between them (GELU included) and the pixel shuffle of the CLIP projector.
 // With rope.hip and the attention kernels, a whole layer stack runs on the
 // GPU from one arena. These follow the reference's session executors
 // (S/graph/session.hpp:287-336, :375-378) and kernels
@@ -86,6 +87,17 @@ __global__ __launch_bounds__(256) void matmul_kernel(const float* w, const float
     }
 }
 
+// GELU as ggml's CPU op computes it (S/kernels/elementwise.hpp:115-167):
+// x <= -10 gives 0, x >= 10 gives x; otherwise x is rounded to binary16 and
+// the tanh approximation of that half, rounded to binary16, is returned --
+// the value ggml's 65536-entry table holds, computed here per element.
+__device__ __forceinline__ float gelu_f16_table(float x) {
+    const float h = static_cast<float>(static_cast<_Float16>(x));
+    const float g = 0.5f * h * (1.0f + tanhf(0.79788456080286535587989211986876f * h * (1.0f + 0.044715f * h * h)));
+    const float t = static_cast<float>(static_cast<_Float16>(g));
+    return x <= -10.0f ? 0.0f : (x >= 10.0f ? x : t);
+}
+
 // Element-wise ops (S/kernels/elementwise.hpp:28-81).
 __global__ __launch_bounds__(256) void elementwise_kernel(const float* a, const float* b, float* out, uint64_t count,
                                                           uint32_t op, float scalar) {
@@ -104,11 +116,78 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const float* a, const 
             // as op_silu followed by op_mul computes it.
             y = (x / (1.0f + expf(-x))) * b[e];
             break;
+        case elementwise_gelu:
+            y = gelu_f16_table(x);
+            break;
         default:  // elementwise_scale
             y = x * scalar;
             break;
         }
         out[e] = y;
+    }
+}
+
+// out = ((x - mean) * (1 / sqrt(var + eps))) * gamma + beta per row, with the
+// reference's accumulation: the mean from a double sum divided in float, the
+// variance from a double sum of the float squared deviations
+// (S/kernels/elementwise.hpp:240-305).
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float* in, const float* gamma, const float* beta,
+                                                         float* out, uint32_t size, float eps) {
+    __shared__ double part[256];
+    __shared__ float stat;
+    const float* x = in + static_cast<std::size_t>(blockIdx.x) * size;
+    float* y = out + static_cast<std::size_t>(blockIdx.x) * size;
+    const auto block_sum = [&](double s) {
+        part[threadIdx.x] = s;
+        __syncthreads();
+        for (uint32_t k = 128; k > 0; k >>= 1) {
+            if (threadIdx.x < k) {
+                part[threadIdx.x] += part[threadIdx.x + k];
+            }
+            __syncthreads();
+        }
+        const double r = part[0];
+        __syncthreads();
+        return r;
+    };
+    double s = 0.0;
+    for (uint32_t e = threadIdx.x; e < size; e += 256) {
+        s += static_cast<double>(x[e]);
+    }
+    const double sum = block_sum(s);
+    if (threadIdx.x == 0) {
+        stat = static_cast<float>(sum) / static_cast<float>(size);
+    }
+    __syncthreads();
+    const float mean = stat;
+    double q = 0.0;
+    for (uint32_t e = threadIdx.x; e < size; e += 256) {
+        const float d = x[e] - mean;
+        q += static_cast<double>(d * d);
+    }
+    const double sq = block_sum(q);
+    const float scale = 1.0f / sqrtf(static_cast<float>(sq / static_cast<double>(size)) + eps);
+    for (uint32_t e = threadIdx.x; e < size; e += 256) {
+        const float v = ((x[e] - mean) * scale) * gamma[e];
+        y[e] = beta != nullptr ? v + beta[e] : v;
+    }
+}
+
+// Merge each s x s block of a grid_w x grid_h grid of patch rows (n floats
+// each, patch x + grid_w * y) into one row of s^2 n floats: out row
+// bx + (grid_w / s) by holds patch (bx s + dx, by s + dy) at offset
+// (dy s + dx) n (kernels::pixel_shuffle, S/kernels/elementwise.hpp:307-333).
+__global__ __launch_bounds__(256) void pixel_shuffle_kernel(const float* in, float* out, uint32_t n, uint32_t grid_w,
+                                                            uint32_t s, uint64_t count) {
+    const uint32_t bw = grid_w / s;
+    const uint64_t merged = uint64_t{s} * s * n;
+    for (uint64_t e = blockIdx.x * 256ull + threadIdx.x; e < count; e += gridDim.x * 256ull) {
+        const uint64_t orow = e / merged;
+        const uint32_t within = static_cast<uint32_t>(e % merged);
+        const uint32_t sub = within / n, k = within % n;
+        const uint32_t bx = static_cast<uint32_t>(orow % bw), by = static_cast<uint32_t>(orow / bw);
+        const uint32_t dy = sub / s, dx = sub % s;
+        out[e] = in[(static_cast<uint64_t>(bx * s + dx) + uint64_t{grid_w} * (by * s + dy)) * n + k];
     }
 }
 
@@ -136,6 +215,19 @@ hipError_t launch_matmul(const float* w, const float* x, const float* bias, floa
                          uint32_t cols, hipStream_t stream) {
     const dim3 grid((rows + 3) / 4, n);
     matmul_kernel<<<grid, 256, 0, stream>>>(w, x, bias, out, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_layer_norm(const float* in, const float* gamma, const float* beta, float* out, uint32_t n,
+                             uint32_t size, float eps, hipStream_t stream) {
+    layer_norm_kernel<<<n, 256, 0, stream>>>(in, gamma, beta, out, size, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_pixel_shuffle(const float* in, float* out, uint32_t n, uint32_t grid_w, uint32_t grid_h, uint32_t s,
+                                hipStream_t stream) {
+    const uint64_t count = uint64_t{grid_w} * grid_h * n;
+    pixel_shuffle_kernel<<<grid_for(count), 256, 0, stream>>>(in, out, n, grid_w, s, count);
     return hipGetLastError();
 }
 

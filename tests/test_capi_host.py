@@ -49,7 +49,8 @@ def test_descriptor_layouts_match_the_header(tmp_path):
     structs = {"syn_kv_desc": capi.KvDesc, "syn_attn_desc": capi.AttnDesc, "syn_seq_desc": capi.SeqDesc,
                "syn_self_desc": capi.SelfDesc, "syn_rope_desc": capi.RopeDesc, "syn_embed_desc": capi.EmbedDesc,
                "syn_norm_desc": capi.NormDesc, "syn_matmul_desc": capi.MatmulDesc,
-               "syn_elementwise_desc": capi.ElementwiseDesc}
+               "syn_elementwise_desc": capi.ElementwiseDesc, "syn_layer_norm_desc": capi.LayerNormDesc,
+               "syn_pixel_shuffle_desc": capi.PixelShuffleDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, ct in structs.items():
         lines.append(f'printf("{cname} @sizeof %zu\\n", sizeof({cname}));')

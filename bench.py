@@ -1,6 +1,6 @@
 """Benchmark of the KV-cache attention path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only decode|prefill|ragged|vision]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only decode|prefill|ragged|vision|gemv]
 
 A step is one decode-attention op of config 2 (Llama-3-8B shape: 32 query
 heads on 8 KV heads, hd 128, 4096 cached rows), through the C ABI: the
@@ -13,7 +13,7 @@ in HBM before the timed region.
 One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time),
 roofline of the decode op (the same HIP-event time on the arena's stream),
 the CPU oracle timed on this host, and the other configs' figures (prefill
-TFLOP/s, ragged decode, ViT) under "extra". --copy-bytes N adds one arena
+TFLOP/s, ragged decode, ViT, quantized GEMV) under "extra". --copy-bytes N adds one arena
 copy of N bytes, the calibration dispatch for rocprofv3 --pmc FETCH_SIZE /
 WRITE_SIZE runs.
 """
@@ -214,6 +214,52 @@ def bench_vision(hip: Hip, cfg: wl.Vision, reps: int):
     return ms
 
 
+# Quantized GEMV shapes of a Llama-3-8B Q4_K_M decode step (one token):
+# (name, ggml type, rows, cols). ffn_gate/up are Q4_K, ffn_down Q6_K; Q8_0
+# is the all-Q8_0 file's.
+GEMV_SHAPES = [("ffn_up Q4_K", 12, 14336, 4096), ("ffn_down Q6_K", 14, 4096, 14336),
+               ("ffn_up Q8_0", 8, 14336, 4096), ("attn_q Q4_K", 12, 4096, 4096)]
+GEMV_BLOCK = {12: (256, 144), 14: (256, 210), 8: (32, 34)}
+
+
+def bench_gemv(hip: Hip, reps: int):
+    """syn_hip_matmul_q for one token (activation quantizer + GEMV) over
+    distinct copies of each weight matrix (>= 320 MB together, past the
+    Infinity Cache). Bytes = weights + x + quantized activations + out."""
+    out = {}
+    g = wl.rng(wl.SEED + 21)
+    for name, t, rows, cols in GEMV_SHAPES:
+        bs, ts = GEMV_BLOCK[t]
+        wbytes = rows * (cols // bs) * ts
+        copies = max(2, -(-(320 << 20) // wbytes))
+        act_bytes = int(lib().syn_hip_matmul_q_act_bytes(t, 1, cols))
+        arena = Arena(copies * capi.align(wbytes) + cols * 4 + act_bytes + rows * 4 + (4 << 20))
+        raw = g.integers(0, 256, size=wbytes, dtype=np.uint8)
+        w_offs = [arena.put(raw) for _ in range(copies)]
+        x_off = arena.put(wl.normal(g, (cols,)))
+        act_off = arena.alloc(act_bytes)
+        out_off = arena.alloc(rows * 4)
+        descs = [capi.MatmulQDesc(w_offset=o, x_offset=x_off, act_offset=act_off, bias_offset=capi.NO_OFFSET,
+                                  out_offset=out_off, w_type=t, n=1, rows=rows, cols=cols) for o in w_offs]
+        L = lib()
+        for d in descs:
+            check(L.syn_hip_matmul_q(arena.handle, ctypes.byref(d)))
+        arena.sync()
+        t0, t1 = hip.events(2)
+        hip.record(t0, arena.stream)
+        for i in range(reps):
+            check(L.syn_hip_matmul_q(arena.handle, ctypes.byref(descs[i % copies])))
+        hip.record(t1, arena.stream)
+        ms = hip.ms(t0, t1) / reps
+        arena.close()
+        nbytes = wbytes + cols * 4 + 2 * act_bytes + rows * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"rows": rows, "cols": cols, "us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                     "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+        log(f"gemv {name} {rows}x{cols}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+    return out
+
+
 def cpu_baseline(cfg: wl.Decode, budget_s: float):
     """The CPU oracle (oracle/liboracle.so, a port of the reference's
     attention()) timed on this host: full config-2 decode steps, threads over
@@ -249,7 +295,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="same as --only decode")
-    ap.add_argument("--only", choices=["decode", "prefill", "ragged", "vision"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "ragged", "vision", "gemv"], default=None,
                     help="run one configuration (no JSON line unless it is decode)")
     ap.add_argument("--copy-bytes", type=int, default=0, help="one arena copy of this many bytes (PMC calibration)")
     args = ap.parse_args()
@@ -292,6 +338,8 @@ def main() -> int:
                            "gbs": round(vcfg.bytes() / (vms * 1e-3) / 1e9, 1),
                            "images_per_s": round(vcfg.batch / (vms * 1e-3), 0)}
         log(f"vision: {vms * 1e3:.1f} us, {extra['vision']['tflops']:.0f} TFLOP/s")
+    if only in (None, "gemv"):
+        extra["gemv_q"] = bench_gemv(hip, 400)
     if only not in (None, "decode"):
         return 0
 

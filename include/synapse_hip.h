@@ -200,14 +200,26 @@ int syn_hip_rope(syn_arena* arena, const syn_rope_desc* desc);
  * With syn_hip_rope and syn_hip_attention these run a whole layer stack from
  * one arena (all rows f32). */
 
+/* Weight formats, by their GGUF (ggml) type numbers and block layouts. */
+enum {
+    SYN_TYPE_F32 = 0,
+    SYN_TYPE_Q4_0 = 2,  /* 32 per 18-byte block */
+    SYN_TYPE_Q5_0 = 6,  /* 32 per 22-byte block */
+    SYN_TYPE_Q8_0 = 8,  /* 32 per 34-byte block */
+    SYN_TYPE_Q4_K = 12, /* 256 per 144-byte block */
+    SYN_TYPE_Q6_K = 14  /* 256 per 210-byte block */
+};
+
 /* Embedding rows: out row i = table row tokens[i] (tokens from host memory,
- * each checked < n_table_rows). Replaces session::execute(const op_embed&),
+ * each checked < n_table_rows; quantized rows dequantized as ggml does). Replaces session::execute(const op_embed&),
  * S/graph/session.hpp:331-336. */
 typedef struct syn_embed_desc {
-    uint64_t table_offset; /* n_table_rows rows of size f32 */
+    uint64_t table_offset; /* n_table_rows rows of size elements of table_type */
     uint64_t out_offset;   /* n rows of size f32 */
     uint32_t n_table_rows;
     uint32_t size;
+    uint32_t table_type;   /* SYN_TYPE_F32, or a quantized SYN_TYPE_* (rows dequantized) */
+    uint32_t reserved;
 } syn_embed_desc;
 
 int syn_hip_embed(syn_arena* arena, const syn_embed_desc* desc, const uint32_t* tokens, uint32_t n);
@@ -242,6 +254,27 @@ typedef struct syn_matmul_desc {
 } syn_matmul_desc;
 
 int syn_hip_matmul(syn_arena* arena, const syn_matmul_desc* desc);
+
+/* Product with quantized weights, as ggml computes it: x is quantized to the
+ * format ggml pairs with w_type (Q8_0 for Q4_0 / Q5_0 / Q8_0, Q8_K for Q4_K /
+ * Q6_K; ggml's reference quantizers, into act), then each weight block meets
+ * its activation block in an exact integer dot, combined in float with the
+ * block scales. Replaces execute(const op_matmul&) for quantized weights,
+ * S/graph/session.hpp:287-302 (S/kernels/gemm.hpp, dot.hpp). */
+typedef struct syn_matmul_q_desc {
+    uint64_t w_offset;    /* rows rows of cols in w_type blocks */
+    uint64_t x_offset;    /* n rows of cols f32 */
+    uint64_t act_offset;  /* scratch of syn_hip_matmul_q_act_bytes(w_type, n, cols) */
+    uint64_t bias_offset; /* rows f32, or UINT64_MAX for none */
+    uint64_t out_offset;  /* n rows of rows f32 */
+    uint32_t w_type;      /* SYN_TYPE_Q* */
+    uint32_t n;
+    uint32_t rows;
+    uint32_t cols;        /* a multiple of the format's block */
+} syn_matmul_q_desc;
+
+uint64_t syn_hip_matmul_q_act_bytes(uint32_t w_type, uint32_t n, uint32_t cols);
+int syn_hip_matmul_q(syn_arena* arena, const syn_matmul_q_desc* desc);
 
 /* Element-wise over count floats (S/kernels/elementwise.hpp:28-81, :115-167):
  * SYN_ADD a + b (op_add, and op_add_rows over whole tables), SYN_MUL a * b

@@ -48,7 +48,13 @@ class RopeDesc(ctypes.Structure):
 
 
 class EmbedDesc(ctypes.Structure):
-    _fields_ = [("table_offset", u64), ("out_offset", u64), ("n_table_rows", u32), ("size", u32)]
+    _fields_ = [("table_offset", u64), ("out_offset", u64), ("n_table_rows", u32), ("size", u32),
+                ("table_type", u32), ("reserved", u32)]
+
+
+class MatmulQDesc(ctypes.Structure):
+    _fields_ = [("w_offset", u64), ("x_offset", u64), ("act_offset", u64), ("bias_offset", u64),
+                ("out_offset", u64), ("w_type", u32), ("n", u32), ("rows", u32), ("cols", u32)]
 
 
 class NormDesc(ctypes.Structure):
@@ -106,6 +112,8 @@ SIGNATURES = {
     "syn_hip_rms_norm": (i32, [ctypes.c_void_p, ctypes.POINTER(NormDesc)]),
     "syn_hip_matmul": (i32, [ctypes.c_void_p, ctypes.POINTER(MatmulDesc)]),
     "syn_hip_elementwise": (i32, [ctypes.c_void_p, ctypes.POINTER(ElementwiseDesc)]),
+    "syn_hip_matmul_q_act_bytes": (u64, [u32, u32, u32]),
+    "syn_hip_matmul_q": (i32, [ctypes.c_void_p, ctypes.POINTER(MatmulQDesc)]),
     "syn_hip_layer_norm": (i32, [ctypes.c_void_p, ctypes.POINTER(LayerNormDesc)]),
     "syn_hip_pixel_shuffle": (i32, [ctypes.c_void_p, ctypes.POINTER(PixelShuffleDesc)]),
 }

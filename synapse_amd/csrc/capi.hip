@@ -736,10 +736,16 @@ int syn_hip_embed(syn_arena* a, const syn_embed_desc* d, const uint32_t* tokens,
     if (d->size == 0 || d->n_table_rows == 0) {
         return fail(SYN_HIP_EINVAL, "embed: %u rows of size %u", d->n_table_rows, d->size);
     }
+    const bool quantized = d->table_type != SYN_TYPE_F32;
+    if (quantized && (!syn::qtype_known(d->table_type) || d->size % syn::qtype_block(d->table_type) != 0)) {
+        return fail(SYN_HIP_EINVAL, "embed: table type %u with rows of %u", d->table_type, d->size);
+    }
     if (n == 0) {
         return SYN_HIP_OK;
     }
-    if (int e = check_range(a, d->table_offset, uint64_t{d->n_table_rows} * d->size * 4, 4, "embed table")) {
+    const uint64_t row_bytes = quantized ? syn::qtype_row_bytes(d->table_type, d->size) : uint64_t{d->size} * 4;
+    if (int e = check_range(a, d->table_offset, uint64_t{d->n_table_rows} * row_bytes, quantized ? 1 : 4,
+                            "embed table")) {
         return e;
     }
     if (int e = check_range(a, d->out_offset, uint64_t{n} * d->size * 4, 4, "embed out")) {
@@ -750,14 +756,18 @@ int syn_hip_embed(syn_arena* a, const syn_embed_desc* d, const uint32_t* tokens,
             return fail(SYN_HIP_EINVAL, "embed: token %u at %u, table has %u rows", tokens[i], i, d->n_table_rows);
         }
     }
-    const auto* table = reinterpret_cast<const float*>(a->base + d->table_offset);
     auto* out = reinterpret_cast<float*>(a->base + d->out_offset);
     for (uint32_t i0 = 0; i0 < n; i0 += syn::embed_max_tokens) {
         const uint32_t m = std::min(n - i0, syn::embed_max_tokens);
         syn::embed_tokens t{};
         std::copy(tokens + i0, tokens + i0 + m, t.token);
-        if (int e = hip_status(syn::launch_embed(table, out + uint64_t{i0} * d->size, t, m, d->size, a->stream),
-                               "embed launch")) {
+        float* dst = out + uint64_t{i0} * d->size;
+        const char* table = a->base + d->table_offset;
+        const hipError_t err =
+            quantized ? syn::launch_embed_q(d->table_type, reinterpret_cast<const uint8_t*>(table), dst, t, m, d->size,
+                                            a->stream)
+                      : syn::launch_embed(reinterpret_cast<const float*>(table), dst, t, m, d->size, a->stream);
+        if (int e = hip_status(err, "embed launch")) {
             return e;
         }
     }
@@ -833,6 +843,68 @@ int syn_hip_matmul(syn_arena* a, const syn_matmul_desc* d) {
                                          reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->rows, d->cols,
                                          a->stream),
                       "matmul launch");
+}
+
+uint64_t syn_hip_matmul_q_act_bytes(uint32_t w_type, uint32_t n, uint32_t cols) {
+    if (!syn::qtype_known(w_type) || cols % syn::qtype_block(w_type) != 0) {
+        return 0;
+    }
+    return syn::qtype_act_bytes(w_type, n, cols);
+}
+
+int syn_hip_matmul_q(syn_arena* a, const syn_matmul_q_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (!syn::qtype_known(d->w_type)) {
+        return fail(SYN_HIP_EUNSUPPORTED, "matmul_q: weight type %u", d->w_type);
+    }
+    if (d->rows == 0 || d->cols == 0 || d->cols % syn::qtype_block(d->w_type) != 0 || d->n > 65535 ||
+        syn::qtype_row_bytes(d->w_type, d->cols) >= (uint64_t{1} << 31)) {
+        return fail(SYN_HIP_EINVAL, "matmul_q: %u x %u weights of type %u, %u rows", d->rows, d->cols, d->w_type,
+                    d->n);
+    }
+    if (d->n == 0) {
+        return SYN_HIP_OK;
+    }
+    const uint64_t x_bytes = uint64_t{d->n} * d->cols * 4;
+    const uint64_t out_bytes = uint64_t{d->n} * d->rows * 4;
+    const uint64_t act_bytes = syn::qtype_act_bytes(d->w_type, d->n, d->cols);
+    if (int e = check_range(a, d->w_offset, uint64_t{d->rows} * syn::qtype_row_bytes(d->w_type, d->cols), 1,
+                            "matmul_q w")) {
+        return e;
+    }
+    if (int e = check_range(a, d->x_offset, x_bytes, 4, "matmul_q x")) {
+        return e;
+    }
+    if (int e = check_range(a, d->act_offset, act_bytes, 1, "matmul_q act")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, out_bytes, 4, "matmul_q out")) {
+        return e;
+    }
+    const auto overlap = [](uint64_t p, uint64_t pn, uint64_t q, uint64_t qn) { return p < q + qn && q < p + pn; };
+    if (overlap(d->act_offset, act_bytes, d->x_offset, x_bytes) ||
+        overlap(d->act_offset, act_bytes, d->out_offset, out_bytes) ||
+        overlap(d->act_offset, act_bytes, d->w_offset, uint64_t{d->rows} * syn::qtype_row_bytes(d->w_type, d->cols))) {
+        return fail(SYN_HIP_EINVAL, "matmul_q: act overlaps an operand");
+    }
+    const float* bias = nullptr;
+    if (d->bias_offset != no_offset) {
+        if (int e = check_range(a, d->bias_offset, uint64_t{d->rows} * 4, 4, "matmul_q bias")) {
+            return e;
+        }
+        bias = reinterpret_cast<const float*>(a->base + d->bias_offset);
+    }
+    return hip_status(syn::launch_matmul_q(d->w_type, reinterpret_cast<const uint8_t*>(a->base + d->w_offset),
+                                           reinterpret_cast<const float*>(a->base + d->x_offset),
+                                           reinterpret_cast<uint8_t*>(a->base + d->act_offset), bias,
+                                           reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->rows, d->cols,
+                                           a->stream),
+                      "matmul_q launch");
 }
 
 int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {

@@ -141,6 +141,16 @@ hipError_t launch_matmul(const float* w, const float* x, const float* bias, floa
                          uint32_t cols, hipStream_t stream);
 hipError_t launch_elementwise(const float* a, const float* b, float* out, uint64_t count, uint32_t op, float scalar,
                               hipStream_t stream);
+// Quantized weights (quant.hip), ggml type numbers.
+constexpr uint32_t qtype_q4_0 = 2, qtype_q5_0 = 6, qtype_q8_0 = 8, qtype_q4_k = 12, qtype_q6_k = 14;
+bool qtype_known(uint32_t t);
+uint32_t qtype_block(uint32_t t);                                   // elements per block
+uint64_t qtype_row_bytes(uint32_t t, uint32_t cols);                // bytes of one row of cols
+uint64_t qtype_act_bytes(uint32_t t, uint32_t n, uint32_t cols);    // quantized activations of n rows
+hipError_t launch_matmul_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
+                           uint32_t n, uint32_t rows, uint32_t cols, hipStream_t stream);
+hipError_t launch_embed_q(uint32_t t, const uint8_t* table, float* out, const embed_tokens& tk, uint32_t n,
+                          uint32_t size, hipStream_t stream);
 hipError_t launch_layer_norm(const float* in, const float* gamma, const float* beta, float* out, uint32_t n,
                              uint32_t size, float eps, hipStream_t stream);
 hipError_t launch_pixel_shuffle(const float* in, float* out, uint32_t n, uint32_t grid_w, uint32_t grid_h, uint32_t s,

@@ -26,7 +26,15 @@ _SCALAR = {_U8: "<B", _I8: "<b", _U16: "<H", _I16: "<h", _U32: "<I", _I32: "<i",
 
 # Tensor types (ggml_type) this build reads.
 F32, F16 = 0, 1
+Q4_0, Q5_0, Q8_0, Q4_K, Q6_K, Q8_K, BF16 = 2, 6, 8, 12, 14, 15, 30
 _DTYPE = {F32: np.float32, F16: np.float16}
+
+# ggml_type -> (elements per block, bytes per block): the published block
+# layouts (ggml-common.h). Types not listed are refused.
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34),
+         Q4_K: (256, 144), Q6_K: (256, 210), Q8_K: (256, 292)}
+TYPE_NAMES = {F32: "F32", F16: "F16", BF16: "BF16", Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K",
+              Q6_K: "Q6_K", Q8_K: "Q8_K"}
 
 
 class GGUFError(ValueError):
@@ -117,6 +125,25 @@ class GGUFFile:
     # ---- tensors --------------------------------------------------------------
     def has(self, name: str) -> bool:
         return name in self.tensors
+
+    def raw(self, name: str) -> tuple[np.ndarray, int, int, int]:
+        """The tensor's bytes as stored: (uint8 array, ggml type, row length
+        ne[0], number of rows). Rows are ne[0] / block elements blocks each."""
+        info = self.tensors.get(name)
+        if info is None:
+            raise GGUFError(f"{self.path}: no tensor {name}")
+        if info.type not in BLOCK:
+            raise GGUFError(f"{self.path}: tensor {name} has unsupported type {info.type}")
+        bs, ts = BLOCK[info.type]
+        row = info.shape[0]
+        if row % bs:
+            raise GGUFError(f"{self.path}: tensor {name}: row of {row} is not whole blocks of {bs}")
+        n_rows = info.n_elements // row
+        nbytes = n_rows * (row // bs) * ts
+        start = self.data_start + info.offset
+        if start + nbytes > len(self._buf):
+            raise GGUFError(f"{self.path}: tensor {name} past the end of the file")
+        return np.frombuffer(self._buf, dtype=np.uint8, count=nbytes, offset=start), info.type, row, n_rows
 
     def tensor(self, name: str) -> np.ndarray:
         """The tensor as an array of shape reversed(ne): rows last-dimension

@@ -15,8 +15,11 @@ The graph is the reference's (S/models/llama.hpp:8-14, built at :405-473):
 
 `read_config` follows the reference's read_llama_config
 (S/models/llama.hpp:125-319) for the keys the three architectures use, in
-float arithmetic as the reference computes them. Weights must be F32 (the
-all-F32 fixtures); quantized weights are refused.
+float arithmetic as the reference computes them. Norms, biases and RoPE
+factors must be F32; the matrices (token embedding, projections, output)
+may be F32 or one of the block formats Q4_0, Q5_0, Q8_0, Q4_K, Q6_K, which
+stay in their GGUF bytes on the device and run through the quantized GEMV
+(activation quantized to Q8_0 / Q8_K, integer block dots).
 """
 from __future__ import annotations
 
@@ -28,8 +31,8 @@ import numpy as np
 
 from . import capi
 from .capi import (NO_OFFSET, SYN_ADD, SYN_F32, SYN_SCALE, SYN_SILU_MUL, Arena, AttnDesc, ElementwiseDesc, EmbedDesc,
-                   MatmulDesc, NormDesc, RopeDesc, check, lib)
-from .gguf import F32, GGUFError, GGUFFile
+                   MatmulDesc, MatmulQDesc, NormDesc, RopeDesc, check, lib)
+from .gguf import F32, Q4_0, Q4_K, Q5_0, Q6_K, Q8_0, TYPE_NAMES, GGUFError, GGUFFile
 
 _f32 = np.float32
 
@@ -161,6 +164,26 @@ def read_config(f: GGUFFile) -> LlamaConfig:
     return c
 
 
+# Block formats the device GEMV and embedding read.
+QUANT_TYPES = (Q4_0, Q5_0, Q8_0, Q4_K, Q6_K)
+
+
+def _matrix(f: GGUFFile, name: str, rows: int, cols: int):
+    """A weight matrix as (ggml type, array to upload): F32 values, or the
+    rows of blocks exactly as the file stores them."""
+    info = f.tensors.get(name)
+    if info is None:
+        raise GGUFError(f"missing tensor {name}")
+    if info.type == F32:
+        return F32, _f32_weight(f, name, (rows, cols))
+    if info.type not in QUANT_TYPES:
+        raise GGUFError(f"{name}: type {TYPE_NAMES.get(info.type, info.type)} is not supported")
+    raw, t, row, n_rows = f.raw(name)
+    if (n_rows, row) != (rows, cols):
+        raise GGUFError(f"{name}: shape {(n_rows, row)}, expected {(rows, cols)}")
+    return t, raw
+
+
 def _f32_weight(f: GGUFFile, name: str, shape) -> np.ndarray:
     info = f.tensors.get(name)
     if info is None:
@@ -193,9 +216,14 @@ class DeviceLlama:
                     and suffix not in biases:
                 raise GGUFError(f"{name}: not supported for {c.arch}")
         self._host = {}
+        self.wtype = {}  # matrix name -> (ggml type, columns)
 
         def w(name, shape):
-            self._host[name] = _f32_weight(f, name, shape)
+            if len(shape) == 2:
+                t, self._host[name] = _matrix(f, name, *shape)
+                self.wtype[name] = (t, shape[1])
+            else:
+                self._host[name] = _f32_weight(f, name, shape)
 
         w("token_embd.weight", (V, E))
         w("output_norm.weight", (E,))
@@ -226,12 +254,16 @@ class DeviceLlama:
         act = {"x": E, "h": E, "q": q_rows, "qr": q_rows, "k": kv_rows, "kr": kv_rows, "v": kv_rows,
                "attn": q_rows, "o": E, "gate": F, "up": F, "down": E, "logits": V}
         scratch_bytes = int(lib().syn_hip_attention_scratch_bytes(c.n_head, c.n_head_kv, hd, max_ctx, 1))
+        # One activation-quantization buffer serves every quantized matrix.
+        qact_bytes = max([int(lib().syn_hip_matmul_q_act_bytes(t, 1, cols))
+                          for t, cols in self.wtype.values() if t != F32] or [0])
         total = sum(capi.align(a.nbytes) for a in self._host.values())
-        total += sum(capi.align(n * 4) for n in act.values())
+        total += sum(capi.align(n * 4) for n in act.values()) + capi.align(max(qact_bytes, 1))
         total += c.n_layer * capi.align(capi.kv_state_bytes(max_ctx, c.n_head_kv, hd)) + capi.align(scratch_bytes)
         self.arena = Arena(total + 4096)
         self.off = {name: self.arena.put(a) for name, a in self._host.items()}
         self.act = {name: self.arena.alloc(n * 4) for name, n in act.items()}
+        self.qact = self.arena.alloc(max(qact_bytes, 1))
         self.caches = [capi.kv_state(self.arena, max_ctx, c.n_head_kv, hd) for _ in range(c.n_layer)]
         self.scratch = (self.arena.alloc(scratch_bytes), scratch_bytes)
         self.theta_scale = rope_theta_scale(c.rope_base, hd)
@@ -252,9 +284,16 @@ class DeviceLlama:
         return self.off.get(name, NO_OFFSET)
 
     def _matmul(self, w, x, out, rows, cols, bias=None):
-        d = MatmulDesc(w_offset=self.off[w], x_offset=self.act[x], bias_offset=self._bias(bias) if bias else NO_OFFSET,
-                       out_offset=self.act[out], n=1, rows=rows, cols=cols)
-        check(lib().syn_hip_matmul(self.arena.handle, ctypes.byref(d)))
+        bias_offset = self._bias(bias) if bias else NO_OFFSET
+        t = self.wtype[w][0]
+        if t == F32:
+            d = MatmulDesc(w_offset=self.off[w], x_offset=self.act[x], bias_offset=bias_offset,
+                           out_offset=self.act[out], n=1, rows=rows, cols=cols)
+            check(lib().syn_hip_matmul(self.arena.handle, ctypes.byref(d)))
+        else:
+            d = MatmulQDesc(w_offset=self.off[w], x_offset=self.act[x], act_offset=self.qact, bias_offset=bias_offset,
+                            out_offset=self.act[out], w_type=t, n=1, rows=rows, cols=cols)
+            check(lib().syn_hip_matmul_q(self.arena.handle, ctypes.byref(d)))
 
     def _norm(self, x, weight, out):
         d = NormDesc(in_offset=self.act[x], weight_offset=self.off[weight], out_offset=self.act[out], n=1,
@@ -282,7 +321,8 @@ class DeviceLlama:
         if not 0 <= pos < self.max_ctx:
             raise ValueError(f"position {pos} outside the {self.max_ctx}-row cache")
         tok = (ctypes.c_uint32 * 1)(token)
-        d = EmbedDesc(table_offset=self.off["token_embd.weight"], out_offset=self.act["x"], n_table_rows=V, size=E)
+        d = EmbedDesc(table_offset=self.off["token_embd.weight"], out_offset=self.act["x"], n_table_rows=V, size=E,
+                      table_type=self.wtype["token_embd.weight"][0])
         check(lib().syn_hip_embed(self.arena.handle, ctypes.byref(d), tok, 1))
         for l in range(c.n_layer):
             b = f"blk.{l}."

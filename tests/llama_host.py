@@ -11,6 +11,7 @@ from __future__ import annotations
 import numpy as np
 
 import binding as orc
+import quant_host as qh
 from synapse_amd.gguf import GGUFFile
 from synapse_amd.llama import attn_temperature, read_config, rope_theta_scale
 
@@ -31,11 +32,41 @@ def silu(x: np.ndarray) -> np.ndarray:
     return (x / (f32(1) + np.exp(-x))).astype(f32)
 
 
+class QuantMatrix:
+    """A weight matrix kept in its GGUF format: rows of blocks."""
+
+    def __init__(self, f: GGUFFile, name: str):
+        self.raw, self.type, self.cols, self.rows = f.raw(name)
+        self.row_bytes = self.raw.size // self.rows
+
+    def row(self, r: int) -> np.ndarray:
+        return self.raw[r * self.row_bytes:(r + 1) * self.row_bytes]
+
+    def matvec(self, x: np.ndarray) -> np.ndarray:
+        """ggml's quantized product: x quantized to the paired activation
+        format, then one integer dot per row."""
+        act = qh.quantize_act(x, self.type)
+        return np.array([qh.vec_dot(self.row(r), self.type, act) for r in range(self.rows)], f32)
+
+    def dequantize_row(self, r: int) -> np.ndarray:
+        return qh.dequantize(self.row(r), self.type)
+
+
+def _weights(f: GGUFFile) -> dict:
+    W = {}
+    for name, info in f.tensors.items():
+        if info.type == 0:
+            W[name] = np.asarray(f.tensor(name), dtype=f32)
+        else:
+            W[name] = QuantMatrix(f, name)
+    return W
+
+
 def decode_logits(f: GGUFFile, tokens, max_ctx: int = 32) -> np.ndarray:
     """Logits after each token, decoded one at a time from position 0."""
     c = read_config(f)
     hd = c.head_dim
-    W = {name: np.asarray(f.tensor(name), dtype=f32) for name in f.tensors}
+    W = _weights(f)
     ff = W.get("rope_freqs.weight")
     s = c.rope_scaling
     scaling = np.array([s.freq_scale, s.ext_factor, s.attn_factor, s.corr_low, s.corr_high], f32)
@@ -44,12 +75,14 @@ def decode_logits(f: GGUFFile, tokens, max_ctx: int = 32) -> np.ndarray:
     caches = [orc.new_cache(max_ctx, c.n_head_kv, hd) for _ in range(c.n_layer)]
 
     def lin(name, x, bias=None):
-        y = (W[name] @ x).astype(f32)
+        w = W[name]
+        y = w.matvec(x) if isinstance(w, QuantMatrix) else (w @ x).astype(f32)
         return (y + W[bias]).astype(f32) if bias in W else y
 
     out = []
     for pos, tok in enumerate(tokens):
-        x = W["token_embd.weight"][tok].copy()
+        embd = W["token_embd.weight"]
+        x = embd.dequantize_row(tok) if isinstance(embd, QuantMatrix) else embd[tok].copy()
         for l in range(c.n_layer):
             b = f"blk.{l}."
             h = rms_norm(x, W[b + "attn_norm.weight"], c.rms_eps)

@@ -814,6 +814,9 @@ int syn_hip_matmul(syn_arena* a, const syn_matmul_desc* d) {
     if (d->rows == 0 || d->cols == 0 || d->n > 65535) {
         return fail(SYN_HIP_EINVAL, "matmul: %u x %u weights, %u rows", d->rows, d->cols, d->n);
     }
+    if (syn::matmul_q_rows_per_pass(1, d->cols) == 0) {
+        return fail(SYN_HIP_EUNSUPPORTED, "matmul_q: %u columns exceed the activation LDS", d->cols);
+    }
     if (d->n == 0) {
         return SYN_HIP_OK;
     }
@@ -867,20 +870,23 @@ int syn_hip_matmul_q(syn_arena* a, const syn_matmul_q_desc* d) {
         return fail(SYN_HIP_EINVAL, "matmul_q: %u x %u weights of type %u, %u rows", d->rows, d->cols, d->w_type,
                     d->n);
     }
+    if (syn::matmul_q_rows_per_pass(1, d->cols) == 0) {
+        return fail(SYN_HIP_EUNSUPPORTED, "matmul_q: %u columns exceed the activation LDS", d->cols);
+    }
     if (d->n == 0) {
         return SYN_HIP_OK;
     }
     const uint64_t x_bytes = uint64_t{d->n} * d->cols * 4;
     const uint64_t out_bytes = uint64_t{d->n} * d->rows * 4;
     const uint64_t act_bytes = syn::qtype_act_bytes(d->w_type, d->n, d->cols);
-    if (int e = check_range(a, d->w_offset, uint64_t{d->rows} * syn::qtype_row_bytes(d->w_type, d->cols), 1,
+    if (int e = check_range(a, d->w_offset, uint64_t{d->rows} * syn::qtype_row_bytes(d->w_type, d->cols), 4,
                             "matmul_q w")) {
         return e;
     }
-    if (int e = check_range(a, d->x_offset, x_bytes, 4, "matmul_q x")) {
+    if (int e = check_range(a, d->x_offset, x_bytes, 16, "matmul_q x")) {
         return e;
     }
-    if (int e = check_range(a, d->act_offset, act_bytes, 1, "matmul_q act")) {
+    if (int e = check_range(a, d->act_offset, act_bytes, 4, "matmul_q act")) {
         return e;
     }
     if (int e = check_range(a, d->out_offset, out_bytes, 4, "matmul_q out")) {

@@ -45,109 +45,7 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& sc, i
     }
 }
 
-// ---- activation quantizers -------------------------------------------------------
-
-// Q8_0, one 32-lane half-wave per block: d = amax / 127 stored as binary16,
-// q = round-half-away-from-zero(x / d).
-__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* x, uint8_t* out, uint64_t n_blocks) {
-    const uint64_t blk = (static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x) / 32;
-    const int l = threadIdx.x & 31;
-    if (blk >= n_blocks) {
-        return;  // whole half-waves
-    }
-    const float v = x[blk * 32 + l];
-    float amax = fabsf(v);
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-    }
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint8_t* b = out + blk * 34;
-    b[2 + l] = static_cast<uint8_t>(static_cast<int8_t>(roundf(v * id)));
-    if (l == 0) {
-        const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
-        b[0] = static_cast<uint8_t>(h & 0xFF);
-        b[1] = static_cast<uint8_t>(h >> 8);
-    }
-}
-
-// Q8_K, one wave per 256-block: max = the first element of largest
-// magnitude, iscale = -127 / max, q = min(127, nearest-even(iscale x)),
-// d = 1 / iscale (f32), and the 16 sums of 16.
-__global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float* x, uint8_t* out, uint64_t n_blocks) {
-    const uint64_t blk = static_cast<uint64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int ln = threadIdx.x & 63;
-    if (blk >= n_blocks) {
-        return;  // wave-uniform
-    }
-    const float* src = x + blk * 256;
-    float v[4];
-    float amax = 0.0f;
-    int at = 256;  // index of the first element with the largest magnitude
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = src[4 * ln + i];
-        const float a = fabsf(v[i]);
-        if (a > amax) {
-            amax = a;
-            at = 4 * ln + i;
-        }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float oa = __shfl_xor(amax, m, wave);
-        const int oi = __shfl_xor(at, m, wave);
-        if (oa > amax || (oa == amax && oi < at)) {
-            amax = oa;
-            at = oi;
-        }
-    }
-    uint8_t* b = out + blk * 292;
-    int8_t q[4] = {0, 0, 0, 0};
-    float d = 0.0f;
-    if (amax != 0.0f) {
-        const float mx = src[at];
-        const float iscale = -127.0f / mx;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q[i] = static_cast<int8_t>(min(127, static_cast<int>(rintf(iscale * v[i]))));
-        }
-        d = 1.0f / iscale;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        b[4 + 4 * ln + i] = static_cast<uint8_t>(q[i]);
-    }
-    // Sum of 16 = 4 lanes of 4.
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, wave);
-    s += __shfl_xor(s, 2, wave);
-    if ((ln & 3) == 0) {
-        const uint16_t u = static_cast<uint16_t>(static_cast<int16_t>(s));
-        b[260 + 2 * (ln >> 2)] = static_cast<uint8_t>(u & 0xFF);
-        b[261 + 2 * (ln >> 2)] = static_cast<uint8_t>(u >> 8);
-    }
-    if (ln == 0) {
-        const uint32_t u = __builtin_bit_cast(uint32_t, d);
-        b[0] = static_cast<uint8_t>(u);
-        b[1] = static_cast<uint8_t>(u >> 8);
-        b[2] = static_cast<uint8_t>(u >> 16);
-        b[3] = static_cast<uint8_t>(u >> 24);
-    }
-}
-
-// ---- the GEMV: one wave per weight row, one lane per 32 weights ------------------
-//
-// A lane's unit is 32 consecutive weights -- a Q4_0 / Q5_0 / Q8_0 block, or
-// one 32-weight slice of a Q4_K / Q6_K super-block -- decoded to 8 dwords of
-// non-negative (or, for Q8_0, signed) int8 values, dotted with the matching
-// 32 activation int8 by v_dot4, and the format's offset (8, 16, 32) taken
-// out through the activation sums. Every integer is exact, so a unit's sum
-// is ggml's; the float combination differs only by association. The wave's
-// loads of one row are contiguous across its lanes; rows are read through a
-// buffer resource of the row's bytes, so the unaligned windows below can
-// over-read the last block and see zeros.
+// ---- buffer loads ------------------------------------------------------------------
 
 __device__ __forceinline__ uint32_t ld32(rsrc r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
@@ -159,22 +57,6 @@ __device__ __forceinline__ uint32_t ld16(rsrc r, uint32_t off) {
 
 __device__ __forceinline__ float half_bits(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
-}
-
-// N dwords of the byte stream at a 2-byte aligned offset: N + 1 aligned
-// dwords realigned with v_alignbyte.
-template <int N>
-__device__ __forceinline__ void window(rsrc r, uint32_t off, uint32_t (&d)[N]) {
-    const uint32_t base = off & ~3u, sh = off & 3u;
-    uint32_t w[N + 1];
-#pragma unroll
-    for (int k = 0; k <= N; ++k) {
-        w[k] = ld32(r, base + 4 * k);
-    }
-#pragma unroll
-    for (int k = 0; k < N; ++k) {
-        d[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], sh);
-    }
 }
 
 __device__ __forceinline__ int dot8(const uint32_t (&a)[8], const uint32_t (&b)[8], int first, int last) {
@@ -191,148 +73,508 @@ __device__ __forceinline__ uint32_t spread4(uint32_t x) {
     return ((x & 1u) << 4) | ((x & 2u) << 11) | ((x & 4u) << 18) | ((x & 8u) << 25);
 }
 
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (static_cast<uint32_t>(a) & 0xFF) | ((static_cast<uint32_t>(b) & 0xFF) << 8) |
+           ((static_cast<uint32_t>(c) & 0xFF) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
 template <uint32_t T>
-constexpr uint32_t block_bytes = T == qtype_q4_0 ? 18 : T == qtype_q5_0 ? 22 : T == qtype_q8_0 ? 34 : T == qtype_q4_k ? 144 : 210;
+constexpr uint32_t block_bytes = T == qtype_q4_0   ? 18
+                                 : T == qtype_q5_0 ? 22
+                                 : T == qtype_q8_0 ? 34
+                                 : T == qtype_q4_k ? 144
+                                                   : 210;
 
 template <uint32_t T>
 constexpr bool k_quant = T == qtype_q4_k || T == qtype_q6_k;
 
+// ---- activations: ggml's reference quantizers, one lane per 32 values -----------
+
+// A lane's 32 quantized activations: the int8 values (4 per dword), the
+// block scale as the dot reads it, and sums of the values (Q8_K: the two
+// sums of 16 it stores; Q8_0: the sum of all 32).
+struct act_unit {
+    uint32_t q[8];
+    float d;
+    int s0, s1;
+};
+
+// x[32u, 32u + 32), loaded apart from its quantization so that the loads
+// can be issued ahead of others.
+struct x_unit {
+    f4 v[8];
+};
+
+__device__ __forceinline__ x_unit load_x(const float* x, uint32_t u) {
+    const f4* src = reinterpret_cast<const f4*>(x + 32 * static_cast<std::size_t>(u));
+    x_unit r;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        r.v[k] = src[k];
+    }
+    return r;
+}
+
+// Q8_0 of one unit: d = amax / 127 stored as binary16,
+// q = round-half-away-from-zero(x / d) (quantize_row_q8_0_ref).
+__device__ __forceinline__ act_unit quantize_q8_0(const x_unit& xu, uint16_t& d_bits) {
+    const f4 (&v)[8] = xu.v;
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            amax = fmaxf(amax, fabsf(v[k][i]));
+        }
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    act_unit a;
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        int q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = static_cast<int>(roundf(v[k][i] * id));
+            sum += q[i];
+        }
+        a.q[k] = pack4(q[0], q[1], q[2], q[3]);
+    }
+    d_bits = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
+    a.d = half_bits(d_bits);
+    a.s0 = sum;
+    a.s1 = 0;
+    return a;
+}
+
+// Q8_K slice u % 8 of super-block u / 8, the super-block's 8 slices on 8
+// consecutive lanes: max = the first element of largest magnitude,
+// iscale = -127 / max, q = min(127, nearest-even(iscale x)), d = 1 / iscale
+// (quantize_row_q8_K_ref).
+__device__ __forceinline__ act_unit quantize_q8_k(const x_unit& xu, uint32_t u) {
+    const f4 (&v)[8] = xu.v;
+    float amax = 0.0f, mx = 0.0f;
+    int at = 1 << 20;  // block index of the first element with the largest magnitude
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = fabsf(v[k][i]);
+            if (a > amax) {
+                amax = a;
+                mx = v[k][i];
+                at = static_cast<int>(32 * (u % 8)) + 4 * k + i;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 1; m <= 4; m <<= 1) {
+        const float oa = __shfl_xor(amax, m, wave);
+        const float om = __shfl_xor(mx, m, wave);
+        const int oi = __shfl_xor(at, m, wave);
+        if (oa > amax || (oa == amax && oi < at)) {
+            amax = oa;
+            mx = om;
+            at = oi;
+        }
+    }
+    act_unit a;
+    if (amax == 0.0f) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            a.q[k] = 0;
+        }
+        a.d = 0.0f;
+        a.s0 = a.s1 = 0;
+        return a;
+    }
+    const float iscale = -127.0f / mx;
+    int s[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        int q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q[i] = min(127, static_cast<int>(rintf(iscale * v[k][i])));
+            s[k / 4] += q[i];
+        }
+        a.q[k] = pack4(q[0], q[1], q[2], q[3]);
+    }
+    a.d = 1.0f / iscale;
+    a.s0 = s[0];
+    a.s1 = s[1];
+    return a;
+}
+
+// ---- weights: a lane's 32 weights, fetched, then decoded for v_dot4 -------------
+//
+// fetch<T> issues the unit's loads and nothing else, so a wave can hold the
+// next batch's loads in flight while it decodes and dots the current one.
+// The 2-byte aligned formats fetch aligned dword windows (one dword more than
+// the stream) that decode realigns with v_alignbyte.
+
+template <uint32_t T>
+struct raw_unit;
+template <>
+struct raw_unit<qtype_q4_k> {
+    u4 h, q0, q1;  // d, dmin, 12 scale bytes; the slice's 32 quant bytes
+};
+template <>
+struct raw_unit<qtype_q6_k> {
+    uint32_t lo[9], hi[9], scp, d;
+};
+template <>
+struct raw_unit<qtype_q8_0> {
+    uint32_t q[9], d;
+};
+template <>
+struct raw_unit<qtype_q4_0> {
+    uint32_t q[5], d;
+};
+template <>
+struct raw_unit<qtype_q5_0> {
+    uint32_t qh[2], q[5], d;
+};
+
+template <int N>
+__device__ __forceinline__ void fetch_window(rsrc r, uint32_t off, uint32_t (&w)[N]) {
+    const uint32_t base = off & ~3u;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        w[k] = ld32(r, base + 4 * k);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void realign(const uint32_t (&w)[N + 1], uint32_t off, uint32_t (&d)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        d[k] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], off & 3u);
+    }
+}
+
+// Unit u of a row whose resource starts delta (0 or 2) bytes before it.
+template <uint32_t T>
+__device__ __forceinline__ raw_unit<T> fetch(rsrc wr, uint32_t delta, uint32_t u) {
+    raw_unit<T> x;
+    if constexpr (T == qtype_q4_k) {
+        const uint32_t b = u / 8 * 144 + delta, s = u % 8;
+        x.h = buffer_load16(wr, b);
+        x.q0 = buffer_load16(wr, b + 16 + 32 * (s / 2));
+        x.q1 = buffer_load16(wr, b + 32 + 32 * (s / 2));
+    } else if constexpr (T == qtype_q6_k) {  // slice s is quarter s % 4 of half s / 4
+        const uint32_t b = u / 8 * 210 + delta, s = u % 8, hf = s / 4, k4 = s % 4;
+        fetch_window(wr, b + 64 * hf + 32 * (k4 & 1), x.lo);
+        fetch_window(wr, b + 128 + 32 * hf, x.hi);
+        x.scp = ld16(wr, b + 192 + 8 * hf + 2 * k4);
+        x.d = ld16(wr, b + 208);
+    } else {
+        const uint32_t b = u * block_bytes<T> + delta;
+        x.d = ld16(wr, b);
+        if constexpr (T == qtype_q5_0) {
+            fetch_window(wr, b + 2, x.qh);
+            fetch_window(wr, b + 6, x.q);
+        } else {
+            fetch_window(wr, b + 2, x.q);
+        }
+    }
+    return x;
+}
+
+// q: 8 dwords of int8 (non-negative, except Q8_0's signed values); the dot
+// is then combined with the scales below.
+struct weight_unit {
+    uint32_t q[8];
+    float d, dmin;
+    int sc0, sc1;  // Q4_K: scale and min; Q6_K: the two 16-weight scales
+};
+
+template <uint32_t T>
+__device__ __forceinline__ weight_unit decode(const raw_unit<T>& r, uint32_t delta, uint32_t u) {
+    constexpr uint32_t nib = 0x0F0F0F0Fu;
+    weight_unit x;
+    x.dmin = 0.0f;
+    x.sc0 = x.sc1 = 0;
+    if constexpr (T == qtype_q4_k) {
+        const uint32_t s = u % 8, shift = (s & 1) * 4;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x.q[k] = (r.q0[k] >> shift) & nib;
+            x.q[4 + k] = (r.q1[k] >> shift) & nib;
+        }
+        const auto byte = [&](uint32_t j) { return (r.h[1 + j / 4] >> (8 * (j % 4))) & 0xFFu; };
+        if (s < 4) {
+            x.sc0 = static_cast<int>(byte(s) & 63);
+            x.sc1 = static_cast<int>(byte(s + 4) & 63);
+        } else {
+            x.sc0 = static_cast<int>((byte(s + 4) & 0xF) | ((byte(s - 4) >> 6) << 4));
+            x.sc1 = static_cast<int>((byte(s + 4) >> 4) | ((byte(s) >> 6) << 4));
+        }
+        x.d = half_bits(r.h[0]);
+        x.dmin = half_bits(r.h[0] >> 16);
+    } else if constexpr (T == qtype_q6_k) {
+        const uint32_t b = u / 8 * 210 + delta, s = u % 8, hf = s / 4, k4 = s % 4;
+        uint32_t lo[8], hi[8];
+        realign(r.lo, b + 64 * hf + 32 * (k4 & 1), lo);
+        realign(r.hi, b + 128 + 32 * hf, hi);
+        const uint32_t lshift = (k4 >> 1) * 4;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            x.q[k] = ((lo[k] >> lshift) & nib) | (((hi[k] >> (2 * k4)) & 0x03030303u) << 4);
+        }
+        x.d = half_bits(r.d);
+        x.sc0 = static_cast<int8_t>(r.scp & 0xFF);
+        x.sc1 = static_cast<int8_t>(r.scp >> 8);
+    } else {
+        const uint32_t b = u * block_bytes<T> + delta;
+        x.d = half_bits(r.d);
+        if constexpr (T == qtype_q8_0) {
+            realign(r.q, b + 2, x.q);
+        } else if constexpr (T == qtype_q4_0) {
+            uint32_t qs[4];
+            realign(r.q, b + 2, qs);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                x.q[k] = qs[k] & nib;
+                x.q[4 + k] = (qs[k] >> 4) & nib;
+            }
+        } else {  // Q5_0
+            uint32_t qh[1], qs[4];
+            realign(r.qh, b + 2, qh);
+            realign(r.q, b + 6, qs);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                x.q[k] = (qs[k] & nib) | spread4((qh[0] >> (4 * k)) & 0xF);
+                x.q[4 + k] = ((qs[k] >> 4) & nib) | spread4((qh[0] >> (16 + 4 * k)) & 0xF);
+            }
+        }
+    }
+    return x;
+}
+
+// One unit's contribution: exact integers, then the scales in float as ggml
+// combines a block.
+template <uint32_t T>
+__device__ __forceinline__ float unit_dot(const weight_unit& w, const act_unit& a) {
+    if constexpr (T == qtype_q4_k) {
+        const int isum = w.sc0 * dot8(w.q, a.q, 0, 8);
+        const int imin = w.sc1 * (a.s0 + a.s1);
+        return (w.d * a.d) * static_cast<float>(isum) - (w.dmin * a.d) * static_cast<float>(imin);
+    } else if constexpr (T == qtype_q6_k) {
+        const int s0 = dot8(w.q, a.q, 0, 4) - 32 * a.s0;
+        const int s1 = dot8(w.q, a.q, 4, 8) - 32 * a.s1;
+        return (w.d * a.d) * static_cast<float>(w.sc0 * s0 + w.sc1 * s1);
+    } else {
+        // The zero point (8 for Q4_0, 16 for Q5_0) comes out through the sum.
+        constexpr int zero = T == qtype_q4_0 ? 8 : (T == qtype_q5_0 ? 16 : 0);
+        const int sumi = dot8(w.q, a.q, 0, 8) - zero * a.s0;
+        return static_cast<float>(sumi) * (w.d * a.d);
+    }
+}
+
+// ---- the fused GEMV -----------------------------------------------------------------
+//
+// out[r][o] = sum_c W[o][c] x[r][c] (+ bias[o]) with ggml's arithmetic: x
+// quantized to the paired activation format (Q8_0 for Q4_0 / Q5_0 / Q8_0,
+// Q8_K for Q4_K / Q6_K), integer block dots, float block combines.
+//
+// One launch. A workgroup of 8 waves first quantizes the NR activation rows
+// into LDS, one lane per 32 values (the 8 lanes of a Q8_K super-block agree
+// on its scale by shuffles); workgroup 0 also stores those blocks, in ggml's
+// layout, into act -- the C ABI's scratch, as the reference's op_matmul
+// leaves them in its scratch. Then each wave streams whole weight rows, one
+// lane per 32 weights (a Q4_0/Q5_0/Q8_0 block or a 32-weight slice of a
+// Q4_K/Q6_K super-block), taking rows blockIdx * 8 + wave, then every
+// gridDim * 8: the grid is sized to stay resident, so the activations are
+// quantized once per workgroup, not once per row. Rows are read through a
+// buffer resource of the row's bytes: the 2-byte aligned formats load
+// aligned dword windows realigned by v_alignbyte, and the last window's
+// over-read sees zeros.
+
+// LDS bytes of NR quantized activation rows: per unit 32 int8, a float
+// scale and two int sums.
+inline __host__ __device__ uint32_t gemv_lds_bytes(uint32_t nr, uint32_t units) {
+    return nr * units * (32 + 4 + 8);
+}
+
 template <uint32_t T, int NR>
-__global__ __launch_bounds__(256) void gemv_q_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
-                                                     float* out, uint32_t n, uint32_t rows, uint32_t cols) {
-    const uint32_t o = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    if (o >= rows) {
-        return;  // wave-uniform
-    }
-    const uint32_t ln = threadIdx.x & 63;
-    const uint32_t r0 = blockIdx.y * NR;
+__global__ __launch_bounds__(512) void gemv_q_kernel(const uint8_t* w, const float* x, uint8_t* act,
+                                                      const float* bias, float* out, uint32_t n, uint32_t rows,
+                                                      uint32_t cols) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
     const uint32_t units = cols / 32;
+    u4* lds_q = reinterpret_cast<u4*>(lds);                                   // [NR][units][2] x 16 B
+    float* lds_d = reinterpret_cast<float*>(lds + NR * units * 32);           // [NR][units]
+    int2* lds_s = reinterpret_cast<int2*>(lds + NR * units * 36);             // [NR][units]
+    const uint32_t r0 = blockIdx.y * NR;
+
+    // ---- whole weight rows, one per wave at a time ----------------------------------------
+    // A wave's work is a sequence of items -- B units per lane of one row --
+    // over its rows (blockIdx * 8 + wave, then every gridDim * 8). Loads run
+    // two items ahead of the one being decoded, and the first two go out
+    // before the activations are quantized. Every load is unconditional:
+    // units past the row, and items past the wave's last, read zeros through
+    // the resource without touching memory, and their products are dropped.
+    constexpr int B = T == qtype_q6_k ? 1 : (T == qtype_q8_0 || T == qtype_q4_k || T == qtype_q5_0 ? 2 : 4);
+    // Wave-uniform (scalar) so that the row resources live in SGPRs.
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ln = threadIdx.x & 63;
     const uint32_t wrow = cols / (k_quant<T> ? 256 : 32) * block_bytes<T>;
-    const uint32_t arow = k_quant<T> ? cols / 256 * 292 : cols / 32 * 34;
-    const rsrc wr = make_rsrc(w + static_cast<std::size_t>(o) * wrow, wrow);
-    rsrc ar[NR];
+    const uint32_t nb = (units + 64 * B - 1) / (64 * B);  // items per row
+    const uint32_t o_step = gridDim.x * 8;
+    const uint32_t o0 = blockIdx.x * 8 + wv;
+    const uint32_t n_items = o0 < rows ? (rows - o0 + o_step - 1) / o_step * nb : 0;
+    struct item_src {
+        rsrc r;
+        uint32_t delta, k;
+    };
+    const auto item = [&](uint32_t t) {
+        item_src x{make_rsrc(w, 0), 0, 0};
+        if (t < n_items) {
+            // Rows of an odd number of 22- or 210-byte blocks start 2 bytes
+            // into a dword: the resource starts at the dword.
+            const uint8_t* rp = w + static_cast<std::size_t>(o0 + t / nb * o_step) * wrow;
+            x.delta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(rp) & 3);
+            x.r = make_rsrc(rp - x.delta, wrow + x.delta);
+            x.k = t % nb;
+        }
+        return x;
+    };
+    raw_unit<T> buf[3][B];
+    item_src src[3];
+    const auto fetch_item = [&](int slot, uint32_t t) {
+        src[slot] = item(t);
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-        // Rows past n (the last group's tail) read row n - 1; never stored.
-        ar[i] = make_rsrc(act + static_cast<std::size_t>(min(r0 + i, n - 1)) * arow, arow);
-    }
-    float acc[NR];
-#pragma unroll
-    for (int i = 0; i < NR; ++i) {
-        acc[i] = 0.0f;
-    }
-    constexpr uint32_t nib = 0x0F0F0F0Fu, ones = 0x01010101u;
-#pragma unroll 2
-    for (uint32_t u = ln; u < units; u += 64) {
-        uint32_t q[8];
+        for (int b = 0; b < B; ++b) {
+            buf[slot][b] = fetch<T>(src[slot].r, src[slot].delta, ln + 64 * (B * src[slot].k + b));
+        }
+    };
+    // ---- the activations, into LDS --------------------------------------------------
+    const auto quantize_store = [&](uint32_t u, int j, const x_unit& xv) __attribute__((always_inline)) {
+        const uint32_t r = min(r0 + j, n - 1);
+        act_unit a;
+        uint16_t d_bits = 0;
         if constexpr (k_quant<T>) {
-            const uint32_t sb = u / 8, s = u % 8;
-            if constexpr (T == qtype_q4_k) {
-                const uint32_t b = sb * 144;
-                const u4 h = buffer_load16(wr, b);  // d, dmin, 12 scale bytes
-                const u4 q0 = buffer_load16(wr, b + 16 + 32 * (s / 2));
-                const u4 q1 = buffer_load16(wr, b + 32 + 32 * (s / 2));
-                const uint32_t shift = (s & 1) * 4;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    q[k] = (q0[k] >> shift) & nib;
-                    q[4 + k] = (q1[k] >> shift) & nib;
-                }
-                const auto byte = [&](uint32_t j) { return (h[1 + j / 4] >> (8 * (j % 4))) & 0xFFu; };
-                int sc, m;
-                if (s < 4) {
-                    sc = static_cast<int>(byte(s) & 63);
-                    m = static_cast<int>(byte(s + 4) & 63);
-                } else {
-                    sc = static_cast<int>((byte(s + 4) & 0xF) | ((byte(s - 4) >> 6) << 4));
-                    m = static_cast<int>((byte(s + 4) >> 4) | ((byte(s) >> 6) << 4));
-                }
-                const float d = half_bits(h[0]), dmin = half_bits(h[0] >> 16);
-#pragma unroll
-                for (int i = 0; i < NR; ++i) {
-                    const uint32_t a = sb * 292;
-                    const float yd = __builtin_bit_cast(float, ld32(ar[i], a));
-                    const u4 y0 = buffer_load16(ar[i], a + 4 + 32 * s);
-                    const u4 y1 = buffer_load16(ar[i], a + 20 + 32 * s);
-                    const uint32_t bs = ld32(ar[i], a + 260 + 4 * s);
-                    const uint32_t y[8] = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
-                    const int isum = sc * dot8(q, y, 0, 8);
-                    const int imin = m * (static_cast<int16_t>(bs & 0xFFFF) + static_cast<int16_t>(bs >> 16));
-                    acc[i] += (d * yd) * static_cast<float>(isum) - (dmin * yd) * static_cast<float>(imin);
-                }
-            } else {  // Q6_K: slice s is quarter s % 4 of half s / 4
-                const uint32_t b = sb * 210, hf = s / 4, k4 = s % 4;
-                uint32_t lo[8], hi[8];
-                window(wr, b + 64 * hf + 32 * (k4 & 1), lo);
-                window(wr, b + 128 + 32 * hf, hi);
-                const uint32_t scp = ld16(wr, b + 192 + 8 * hf + 2 * k4);
-                const float d = half_bits(ld16(wr, b + 208));
-                const uint32_t lshift = (k4 >> 1) * 4;
+            a = quantize_q8_k(xv, u);
+        } else {
+            a = quantize_q8_0(xv, d_bits);
+        }
+        lds_q[2 * (j * units + u)] = u4{a.q[0], a.q[1], a.q[2], a.q[3]};
+        lds_q[2 * (j * units + u) + 1] = u4{a.q[4], a.q[5], a.q[6], a.q[7]};
+        lds_d[j * units + u] = a.d;
+        lds_s[j * units + u] = int2{a.s0, a.s1};
+        if (blockIdx.x == 0 && r0 + j < n) {
+            if constexpr (k_quant<T>) {
+                uint8_t* blk = act + static_cast<std::size_t>(r) * (units / 8) * 292 + std::size_t{u / 8} * 292;
+                const uint32_t s = u % 8;
+                uint32_t* qd = reinterpret_cast<uint32_t*>(blk + 4 + 32 * s);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
-                    q[k] = ((lo[k] >> lshift) & nib) | (((hi[k] >> (2 * k4)) & 0x03030303u) << 4);
+                    qd[k] = a.q[k];
                 }
-                const int sc0 = static_cast<int8_t>(scp & 0xFF), sc1 = static_cast<int8_t>(scp >> 8);
+                *reinterpret_cast<uint32_t*>(blk + 260 + 4 * s) =
+                    (static_cast<uint32_t>(a.s0) & 0xFFFF) | (static_cast<uint32_t>(a.s1) << 16);
+                if (s == 0) {
+                    *reinterpret_cast<float*>(blk) = a.d;
+                }
+            } else {
+                uint16_t* blk = reinterpret_cast<uint16_t*>(act + (static_cast<std::size_t>(r) * units + u) * 34);
+                blk[0] = d_bits;
 #pragma unroll
-                for (int i = 0; i < NR; ++i) {
-                    const uint32_t a = sb * 292;
-                    const float yd = __builtin_bit_cast(float, ld32(ar[i], a));
-                    const u4 y0 = buffer_load16(ar[i], a + 4 + 32 * s);
-                    const u4 y1 = buffer_load16(ar[i], a + 20 + 32 * s);
-                    const uint32_t bs = ld32(ar[i], a + 260 + 4 * s);
-                    const uint32_t y[8] = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
-                    const int s0 = dot8(q, y, 0, 4) - 32 * static_cast<int16_t>(bs & 0xFFFF);
-                    const int s1 = dot8(q, y, 4, 8) - 32 * static_cast<int16_t>(bs >> 16);
-                    acc[i] += (d * yd) * static_cast<float>(sc0 * s0 + sc1 * s1);
+                for (int k = 0; k < 8; ++k) {
+                    blk[1 + 2 * k] = static_cast<uint16_t>(a.q[k]);
+                    blk[2 + 2 * k] = static_cast<uint16_t>(a.q[k] >> 16);
                 }
-            }
-        } else {
-            const uint32_t b = u * block_bytes<T>;
-            const float d = half_bits(ld16(wr, b));
-            int offset = 0;  // the format's zero point, taken out through the activation sum
-            if constexpr (T == qtype_q8_0) {
-                window(wr, b + 2, q);
-            } else if constexpr (T == qtype_q4_0) {
-                uint32_t qs[4];
-                window(wr, b + 2, qs);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    q[k] = qs[k] & nib;
-                    q[4 + k] = (qs[k] >> 4) & nib;
-                }
-                offset = 8;
-            } else {  // Q5_0
-                uint32_t qh[1], qs[4];
-                window(wr, b + 2, qh);
-                window(wr, b + 6, qs);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    q[k] = (qs[k] & nib) | spread4((qh[0] >> (4 * k)) & 0xF);
-                    q[4 + k] = ((qs[k] >> 4) & nib) | spread4((qh[0] >> (16 + 4 * k)) & 0xF);
-                }
-                offset = 16;
-            }
-#pragma unroll
-            for (int i = 0; i < NR; ++i) {
-                const uint32_t a = u * 34;
-                const float da = half_bits(ld16(ar[i], a));
-                uint32_t y[8];
-                window(ar[i], a + 2, y);
-                int sumi = dot8(q, y, 0, 8);
-                if (offset != 0) {
-                    const uint32_t one8[8] = {ones, ones, ones, ones, ones, ones, ones, ones};
-                    sumi -= offset * dot8(one8, y, 0, 8);
-                }
-                acc[i] += static_cast<float>(sumi) * (d * da);
             }
         }
+    };
+    const auto x_row = [&](int j) { return x + static_cast<std::size_t>(min(r0 + j, n - 1)) * cols; };
+    if constexpr (NR <= 2) {
+        // The thread's first activation unit is loaded before the first two
+        // weight items, so waiting for it does not wait for them (memory
+        // operations complete in issue order as the wait counter sees them).
+        x_unit xf[NR];
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            xf[j] = load_x(x_row(j), min(threadIdx.x, units - 1));
+        }
+        fetch_item(0, 0);
+        fetch_item(1, 1);
+        if (threadIdx.x < units) {
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                quantize_store(threadIdx.x, j, xf[j]);
+            }
+        }
+        for (uint32_t u = threadIdx.x + 512; u < units; u += 512) {
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                quantize_store(u, j, load_x(x_row(j), u));
+            }
+        }
+    } else {
+        for (uint32_t u = threadIdx.x; u < units; u += 512) {
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                quantize_store(u, j, load_x(x_row(j), u));
+            }
+        }
+        fetch_item(0, 0);
+        fetch_item(1, 1);
     }
+    // LDS complete; the weight loads stay in flight (a __syncthreads() would
+    // wait for every outstanding memory operation).
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    float acc[NR];
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-        const float s = wave_sum_q(acc[i]);
-        if (ln == 0 && r0 + i < n) {
-            out[static_cast<std::size_t>(r0 + i) * rows + o] = bias != nullptr ? s + bias[o] : s;
+    for (int j = 0; j < NR; ++j) {
+        acc[j] = 0.0f;
+    }
+    // Item t decodes from slot C = t % 3 while item t + 2 loads into slot
+    // (C + 2) % 3. Slots are compile-time (three steps per trip) so the
+    // buffers stay in registers; a trip's steps past the last item run on
+    // zeros and store nothing.
+    const auto step = [&]<int C>(uint32_t t) __attribute__((always_inline)) {
+        fetch_item((C + 2) % 3, t + 2);
+        const bool live = t < n_items;
+        const uint32_t k = src[C].k;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const uint32_t u = ln + 64 * (B * k + b);
+            const uint32_t ua = min(u, units - 1);  // a valid LDS slot; dropped below
+            const weight_unit wu = decode<T>(buf[C][b], src[C].delta, u);
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                act_unit a;
+                const u4 q0 = lds_q[2 * (j * units + ua)], q1 = lds_q[2 * (j * units + ua) + 1];
+                a.q[0] = q0[0], a.q[1] = q0[1], a.q[2] = q0[2], a.q[3] = q0[3];
+                a.q[4] = q1[0], a.q[5] = q1[1], a.q[6] = q1[2], a.q[7] = q1[3];
+                a.d = lds_d[j * units + ua];
+                const int2 sm = lds_s[j * units + ua];
+                a.s0 = sm.x;
+                a.s1 = sm.y;
+                const float c = unit_dot<T>(wu, a);
+                acc[j] += live && u < units ? c : 0.0f;
+            }
         }
+        if (live && k + 1 == nb) {
+            const uint32_t o = o0 + t / nb * o_step;
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                const float s = wave_sum_q(acc[j]);
+                if (ln == 0 && r0 + j < n) {
+                    out[static_cast<std::size_t>(r0 + j) * rows + o] = bias != nullptr ? s + bias[o] : s;
+                }
+                acc[j] = 0.0f;
+            }
+        }
+    };
+    for (uint32_t t = 0; t < n_items; t += 3) {
+        step.template operator()<0>(t);
+        step.template operator()<1>(t + 1);
+        step.template operator()<2>(t + 2);
     }
 }
 
@@ -411,24 +653,48 @@ uint64_t qtype_act_bytes(uint32_t t, uint32_t n, uint32_t cols) {
     return t == qtype_q4_k || t == qtype_q6_k ? uint64_t{n} * (cols / 256) * 292 : uint64_t{n} * (cols / 32) * 34;
 }
 
+uint32_t matmul_q_rows_per_pass(uint32_t n, uint32_t cols) {
+    // Up to 4 activation rows share a pass over the weights, as LDS allows.
+    for (uint32_t nr = n >= 4 ? 4 : (n >= 2 ? 2 : 1); nr >= 1; nr /= 2) {
+        if (gemv_lds_bytes(nr, cols / 32) <= matmul_q_max_lds) {
+            return nr;
+        }
+    }
+    return 0;
+}
+
 hipError_t launch_matmul_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
                            uint32_t n, uint32_t rows, uint32_t cols, hipStream_t stream) {
-    if (t == qtype_q4_k || t == qtype_q6_k) {
-        const uint64_t nb = uint64_t{n} * (cols / 256);
-        quantize_q8_k_kernel<<<static_cast<uint32_t>((nb + 3) / 4), 256, 0, stream>>>(x, act, nb);
-    } else {
-        const uint64_t nb = uint64_t{n} * (cols / 32);
-        quantize_q8_0_kernel<<<static_cast<uint32_t>((nb + 7) / 8), 256, 0, stream>>>(x, act, nb);
+    const uint32_t nr = matmul_q_rows_per_pass(n, cols);
+    if (nr == 0) {
+        return hipErrorInvalidValue;
     }
-    const uint32_t nr = n >= 4 ? 4 : (n >= 2 ? 2 : 1);
-    const dim3 grid((rows + 3) / 4, (n + nr - 1) / nr);
+    const uint32_t lds = gemv_lds_bytes(nr, cols / 32);
+    int dev = 0, cus = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) {
+        return e;
+    }
+    if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev); e != hipSuccess) {
+        return e;
+    }
     const auto go = [&]<uint32_t T>() {
+        const auto run = [&](auto kernel) {
+            // A resident grid: as many 8-wave workgroups as the CUs hold at
+            // once with this kernel's registers and this LDS.
+            int per_cu = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 512, lds) != hipSuccess || per_cu < 1) {
+                per_cu = 1;
+            }
+            const uint32_t resident = static_cast<uint32_t>(cus) * static_cast<uint32_t>(per_cu);
+            const dim3 grid(std::min((rows + 7) / 8, resident), (n + nr - 1) / nr);
+            kernel<<<grid, 512, lds, stream>>>(w, x, act, bias, out, n, rows, cols);
+        };
         if (nr == 4) {
-            gemv_q_kernel<T, 4><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+            run(gemv_q_kernel<T, 4>);
         } else if (nr == 2) {
-            gemv_q_kernel<T, 2><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+            run(gemv_q_kernel<T, 2>);
         } else {
-            gemv_q_kernel<T, 1><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+            run(gemv_q_kernel<T, 1>);
         }
     };
     switch (t) {

@@ -79,7 +79,7 @@ def test_matmul_q_matches_ggml_golden(arena, name):
 
 
 @pytest.mark.parametrize("t", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])
-@pytest.mark.parametrize("n,rows,cols", [(1, 300, 2048), (3, 67, 4096), (2, 5, 256)])
+@pytest.mark.parametrize("n,rows,cols", [(1, 300, 2048), (3, 67, 4096), (2, 5, 256), (5, 9, 512), (1, 6, 20480)])
 def test_matmul_q_matches_host_blocks(arena, t, n, rows, cols):
     rng = np.random.default_rng(1000 * t + rows)
     raw = random_blocks(t, rows, cols, rng)

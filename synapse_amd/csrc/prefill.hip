@@ -359,13 +359,413 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
     }
 }
 
+// ---- balanced causal prefill: pairs of query tiles ----------------------------------
+//
+// Under the causal cut query tile t needs t + 1 key spans, so with one block
+// per tile the latest tile's block runs long after its co-resident partner
+// has finished. Here a block of 8 waves takes a pair of query tiles
+// (r, n_qt - 1 - r) of one head. Wave group 1 (waves 4-7) takes the later
+// tile's last key tiles; wave group 0 (waves 0-3) the earlier tile whole,
+// then the later tile's first key tiles, so the groups do the same number of
+// key tiles (within one). Each group runs the 4-wave kernel's two-stage LDS
+// pipeline on its own stages, 128 queries, a wave 32 of them; both run the
+// same number of steps, so the block-wide barriers pair up. The two partial
+// (max, sum, O) of the later tile's queries meet in LDS at the end, in a
+// fixed order. The tail of the last V^T chunk past kv_end is zeroed by the
+// lane that copied it, right after its copy lands.
+template <int HD, bool QF16>
+__global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a) {
+    constexpr int NS = HD / 16;
+    constexpr int NT = HD / 32;
+    constexpr int HSPAN = HD / 2;
+    constexpr int KCPR = HD / 8;
+    constexpr int KROWC = KCPR + 1;
+    constexpr int VROWC = pf_bk / 8 + 1;
+    constexpr int TK = pf_bk * KROWC / 64;
+    constexpr int TV = (HD * VROWC + 63) / 64;
+    constexpr int TT = TK + TV;
+    // The merge of the two partials takes NT * 16 + 2 floats per lane, 1 KB
+    // each for the group's 256 lanes, from group 0's four stage buffers.
+    static_assert(2 * TK + 2 * TV >= NT * 16 + 2, "merge does not fit the stage buffers");
+    __shared__ __attribute__((aligned(16))) char lk00[TK * 1024];
+    __shared__ __attribute__((aligned(16))) char lk01[TK * 1024];
+    __shared__ __attribute__((aligned(16))) char lv00[TV * 1024];
+    __shared__ __attribute__((aligned(16))) char lv01[TV * 1024];
+    __shared__ __attribute__((aligned(16))) char lk10[TK * 1024];
+    __shared__ __attribute__((aligned(16))) char lk11[TK * 1024];
+    __shared__ __attribute__((aligned(16))) char lv10[TV * 1024];
+    __shared__ __attribute__((aligned(16))) char lv11[TV * 1024];
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int grp = w >> 2;                                   // wave group
+    const int wg = w & 3;                                     // wave inside the group
+    const int ln = tid & 63;
+    const int H = ln >> 5;
+    const int qi = ln & 31;
+    const uint32_t hd = a.hd;
+    const uint32_t n_qt = (a.n + pf_bq - 1) / pf_bq;
+    const uint32_t pr = blockIdx.x / a.n_heads;
+    const uint32_t h = blockIdx.x % a.n_heads;
+    const uint32_t tA = pr, tB = n_qt - 1 - pr;  // tA == tB: the middle tile of an odd count
+    const uint32_t g = h / a.group;
+    const float c = a.scale_log2e;
+
+    const auto kv_end_of = [&](uint32_t qt) __attribute__((always_inline)) {
+        return min(a.kv_len, a.pos + min(a.n, qt * pf_bq + pf_bq));
+    };
+    const uint32_t nA = tA == tB ? 0 : (kv_end_of(tA) + pf_bk - 1) / pf_bk;
+    const uint32_t nB = (kv_end_of(tB) + pf_bk - 1) / pf_bk;
+    const uint32_t half = (nA + nB + 1) / 2;  // group 0's items; nA <= half
+    const uint32_t split = half - nA;         // the later tile's key tiles group 0 takes
+    const uint32_t cnt = grp == 0 ? half : nB - split;
+    // Item j of this group: (query tile, key tile).
+    const auto item_qt = [&](uint32_t j) __attribute__((always_inline)) { return grp == 0 && j < nA ? tA : tB; };
+    const auto item_kt = [&](uint32_t j) __attribute__((always_inline)) {
+        return grp == 0 ? (j < nA ? j : j - nA) : split + j;
+    };
+
+    // The query tile being computed and what follows from it.
+    uint32_t q_row0 = 0, my_q = 0, my_pos = 0, kv_end = 0, wave_last_pos = 0;
+    h8 qv[NS];
+    const auto enter = [&](uint32_t qt) __attribute__((always_inline)) {
+        q_row0 = qt * pf_bq + 32 * wg;
+        my_q = q_row0 + qi;
+        my_pos = a.pos + my_q;
+        kv_end = kv_end_of(qt);
+        wave_last_pos = a.pos + min(a.n - 1, q_row0 + 31);
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const uint32_t d0 = H * HSPAN + 8 * st;
+            qv[st] = my_q < a.n && d0 < hd
+                         ? pf_load_q<QF16>(a.q, static_cast<std::size_t>(my_q) * a.q_row + h * hd + d0)
+                         : as_h8(zero_u4());
+        }
+    };
+
+    // Copy offsets as in the 4-wave kernel, over the group's 4 waves; vc[i]
+    // is the key chunk of a V^T copy (8 keys), or 8 for none.
+    constexpr int CPW = (TT + 3) / 4;
+    uint32_t coff[CPW], vc[CPW];
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+        const uint32_t j = wg + 4 * i;
+        coff[i] = buffer_oob;
+        vc[i] = 8;
+        if (j < TK) {
+            const uint32_t L = 64 * j + ln;
+            const uint32_t r = L / KROWC, cc = L % KROWC;
+            if (cc < KCPR && 8 * cc < hd) {
+                coff[i] = r * a.row * 2 + cc * 16;
+            }
+        } else if (j < TT) {
+            const uint32_t L = 64 * (j - TK) + ln;
+            const uint32_t d = L / VROWC, cc = L % VROWC;
+            if (cc < 8 && d < hd) {
+                coff[i] = d * a.ctx_stride * 2 + cc * 16;
+                vc[i] = cc;
+            }
+        }
+    }
+    const _Float16* k_head = a.k + g * hd;
+    const _Float16* v_head = a.vt + static_cast<std::size_t>(g) * hd * a.ctx_stride;
+    const uint32_t v_bytes = hd * a.ctx_stride * 2;
+    const auto issue = [&](uint32_t j, char* sk, char* sv) __attribute__((always_inline)) {
+        const uint32_t ke = kv_end_of(item_qt(j));
+        const uint32_t t0 = item_kt(j) * pf_bk;
+        const rsrc k_res = make_rsrc(k_head + static_cast<std::size_t>(t0) * a.row, (ke - t0) * a.row * 2 - g * hd * 2);
+        const rsrc v_res = make_rsrc(v_head + t0, v_bytes - t0 * 2);
+        const bool last = t0 + pf_bk > ke;
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
+            const uint32_t jj = wg + 4 * i;
+            if (jj < TK) {
+                pf_copy(k_res, sk + 1024 * jj, coff[i]);
+            } else if (jj < TT) {
+                pf_copy(v_res, sv + 1024 * (jj - TK), last && 8 * vc[i] >= ke - t0 ? buffer_oob : coff[i]);
+            }
+        }
+    };
+    // After item j's copies landed: the V^T chunk straddling kv_end holds
+    // stale halves past it (a zero probability times a stale non-finite half
+    // would be NaN); the lane that copied it zeroes them.
+    const auto tail = [&](uint32_t j, char* sv) __attribute__((always_inline)) {
+        const uint32_t ke = kv_end_of(item_qt(j));
+        const uint32_t t0 = item_kt(j) * pf_bk;
+        if (t0 + pf_bk <= ke || ke % 8 == 0) {
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) {
+            const uint32_t jj = wg + 4 * i;
+            if (jj >= TK && jj < TT && vc[i] == (ke - t0) / 8) {
+                _Float16* chunk = reinterpret_cast<_Float16*>(sv + 1024 * (jj - TK) + 16 * ln);
+                for (uint32_t k = ke % 8; k < 8; ++k) {
+                    chunk[k] = 0;
+                }
+            }
+        }
+    };
+
+    f16v o[NT];
+    float m_run = -INFINITY, l_run = 0.0f;
+    const auto reset = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                o[n][i] = 0.0f;
+            }
+        }
+        m_run = -INFINITY;
+        l_run = 0.0f;
+    };
+    // The normalised rows of the current query tile, to out.
+    const auto store = [&]() __attribute__((always_inline)) {
+        if (my_q >= a.n) {
+            return;
+        }
+        const float inv = 1.0f / l_run;
+        float* out = a.out + static_cast<std::size_t>(my_q) * a.q_row + h * hd;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t d = 32 * n + 8 * b + 4 * H;
+                if (d < hd) {
+                    *reinterpret_cast<f4*>(out + d) =
+                        f4{o[n][4 * b] * inv, o[n][4 * b + 1] * inv, o[n][4 * b + 2] * inv, o[n][4 * b + 3] * inv};
+                }
+            }
+        }
+    };
+
+    // One 64-key tile from one LDS stage (the 4-wave kernel's step).
+    const auto compute = [&](uint32_t t0, const char* sk, const char* sv) __attribute__((always_inline)) {
+        if (q_row0 >= a.n || t0 > wave_last_pos) {
+            return;
+        }
+        f16v sc[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                sc[e][i] = 0.0f;
+            }
+            const char* krow = sk + ((32 * e + pf_slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
+            }
+        }
+        if (t0 + pf_bk - 1 > a.pos + q_row0 || t0 + pf_bk > kv_end) {
+            const uint32_t lim = max(min(my_pos + 1, kv_end), t0) - t0;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t kk = 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
+                    sc[e][i] = kk < lim ? sc[e][i] : -INFINITY;
+                }
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                tmax = fmaxf(tmax, sc[e][i]);
+            }
+        }
+        tmax = max32(tmax);
+        const bool grow = (tmax - m_run) * c > 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = grow ? tmax : m_run;
+            const float alpha = grow ? fast_exp2((m_run - m_new) * c) : 1.0f;
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    o[n][i] *= alpha;
+                }
+            }
+        }
+        const float mc = (m_run == -INFINITY ? 0.0f : m_run) * c;
+        h8 pv[4];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                pv[2 * e + (i >> 3)][i & 7] = to_h(fast_exp2(sc[e][i] * c - mc));
+            }
+        }
+        float psum = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                psum = add_pair(h2{pv[s2][i], pv[s2][i + 1]}, psum);
+            }
+        }
+        l_run += sum32(psum);
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const char* vrow = sv + ((32 * n + qi) * VROWC + H) * 16;
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                o[n] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[n]);
+            }
+        }
+    };
+
+    // This wave's copies per item: TT / 4 or one more.
+    const uint32_t per_tile = (TT - wg + 3) / 4;
+    const auto wait_item = [&](bool next_issued) __attribute__((always_inline)) {
+        if (!next_issued) {
+            __builtin_amdgcn_s_waitcnt(pf_vmcnt(0));
+        } else if (per_tile == (TT + 3) / 4) {
+            __builtin_amdgcn_s_waitcnt(pf_vmcnt((TT + 3) / 4));
+        } else {
+            __builtin_amdgcn_s_waitcnt(pf_vmcnt(TT / 4));
+        }
+    };
+
+    // Item j: switch query tile when it changes (group 0 after the earlier
+    // tile: its rows go out, the later tile's queries come in), then compute.
+    uint32_t cur_qt = item_qt(0);
+    const auto run = [&](uint32_t j, const char* sk, const char* sv) __attribute__((always_inline)) {
+        if (j >= cnt) {
+            return;
+        }
+        const uint32_t qt = item_qt(j);
+        if (qt != cur_qt) {
+            store();
+            reset();
+            enter(qt);
+            cur_qt = qt;
+        }
+        compute(item_kt(j) * pf_bk, sk, sv);
+    };
+    // The group's pipeline over its items; both groups take `half` steps
+    // (two barriers each), so every barrier has all 8 waves.
+    const auto pipeline = [&](char* k0, char* v0, char* k1, char* v1) __attribute__((always_inline)) {
+        if (cnt > 0) {
+            issue(0, k0, v0);
+        }
+        if (cnt > 1) {
+            issue(1, k1, v1);
+        }
+        wait_item(cnt > 1);
+        if (cnt > 0) {
+            tail(0, v0);
+        }
+        pf_barrier();
+        for (uint32_t j = 0; j < half; j += 2) {
+            run(j, k0, v0);
+            pf_barrier();
+            if (j + 2 < cnt) {
+                issue(j + 2, k0, v0);
+            }
+            wait_item(j + 2 < cnt);
+            if (j + 1 < cnt) {
+                tail(j + 1, v1);
+            }
+            pf_barrier();
+            if (j + 1 >= half) {
+                break;
+            }
+            run(j + 1, k1, v1);
+            pf_barrier();
+            if (j + 3 < cnt) {
+                issue(j + 3, k1, v1);
+            }
+            wait_item(j + 3 < cnt);
+            if (j + 2 < cnt) {
+                tail(j + 2, v0);
+            }
+            pf_barrier();
+        }
+    };
+    reset();
+    enter(cur_qt);
+    if (grp == 0) {
+        pipeline(lk00, lv00, lk01, lv01);
+    } else {
+        pipeline(lk10, lv10, lk11, lv11);
+    }
+    // Group 0 may have ended on the earlier tile (it took none of the later
+    // tile's keys): its rows go out and its partial of the later tile is empty.
+    if (grp == 0 && cur_qt != tB) {
+        store();
+        reset();
+        enter(tB);
+    }
+
+    // ---- merge the later tile's two partials: group 0 -> LDS -> group 1 --------------
+    // Float f of lane (wg, ln) sits at index (f * 256 + 64 wg + ln) of group
+    // 0's stage buffers taken in order (lk00, lk01, lv00, lv01): o[n][i] is
+    // f = 16 n + i, then the max and the sum.
+    const auto slot = [&](int f) __attribute__((always_inline)) -> float* {
+        const uint32_t lane = 64 * wg + ln;
+        if (f < TK) {
+            return reinterpret_cast<float*>(lk00) + f * 256 + lane;
+        }
+        if (f < 2 * TK) {
+            return reinterpret_cast<float*>(lk01) + (f - TK) * 256 + lane;
+        }
+        if (f < 2 * TK + TV) {
+            return reinterpret_cast<float*>(lv00) + (f - 2 * TK) * 256 + lane;
+        }
+        return reinterpret_cast<float*>(lv01) + (f - 2 * TK - TV) * 256 + lane;
+    };
+    if (grp == 0) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                *slot(16 * n + i) = o[n][i];
+            }
+        }
+        *slot(16 * NT) = m_run;
+        *slot(16 * NT + 1) = l_run;
+    }
+    pf_barrier();
+    if (grp == 1) {
+        const float m0 = *slot(16 * NT), l0 = *slot(16 * NT + 1);
+        const float m = fmaxf(m0, m_run);
+        const float a0 = m0 == -INFINITY ? 0.0f : fast_exp2((m0 - m) * c);
+        const float a1 = m_run == -INFINITY ? 0.0f : fast_exp2((m_run - m) * c);
+        l_run = l0 * a0 + l_run * a1;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                o[n][i] = *slot(16 * n + i) * a0 + o[n][i] * a1;
+            }
+        }
+        store();
+    }
+}
+
 template <int HD>
 hipError_t launch_hd(const flash_args& a, uint32_t dtype, hipStream_t stream) {
-    const dim3 grid(a.n_heads * ((a.n + pf_bq - 1) / pf_bq));
-    if (dtype == 1) {
-        prefill_kernel<HD, true><<<grid, 256, 0, stream>>>(a);
+    if constexpr (HD <= 128) {
+        // Two wave groups' stages fit LDS up to hd 128.
+        const dim3 grid(a.n_heads * ((a.n + 2 * pf_bq - 1) / (2 * pf_bq)));
+        if (dtype == 1) {
+            prefill_pair_kernel<HD, true><<<grid, 512, 0, stream>>>(a);
+        } else {
+            prefill_pair_kernel<HD, false><<<grid, 512, 0, stream>>>(a);
+        }
     } else {
-        prefill_kernel<HD, false><<<grid, 256, 0, stream>>>(a);
+        const dim3 grid(a.n_heads * ((a.n + pf_bq - 1) / pf_bq));
+        if (dtype == 1) {
+            prefill_kernel<HD, true><<<grid, 256, 0, stream>>>(a);
+        } else {
+            prefill_kernel<HD, false><<<grid, 256, 0, stream>>>(a);
+        }
     }
     return hipGetLastError();
 }

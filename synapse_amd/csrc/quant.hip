@@ -645,7 +645,11 @@ uint32_t qtype_block(uint32_t t) {
 }
 
 uint64_t qtype_row_bytes(uint32_t t, uint32_t cols) {
-    const uint64_t per = t == qtype_q4_0 ? 18 : t == qtype_q5_0 ? 22 : t == qtype_q8_0 ? 34 : t == qtype_q4_k ? 144 : 210;
+    const uint64_t per = t == qtype_q4_0   ? 18
+                         : t == qtype_q5_0 ? 22
+                         : t == qtype_q8_0 ? 34
+                         : t == qtype_q4_k ? 144
+                                           : 210;
     return uint64_t{cols} / qtype_block(t) * per;
 }
 

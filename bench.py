@@ -1,6 +1,6 @@
 """Benchmark of the KV-cache attention path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only decode|prefill|ragged|vision|gemv]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--only decode|prefill|ragged|vision|gemv|gemm]
 
 A step is one decode-attention op of config 2 (Llama-3-8B shape: 32 query
 heads on 8 KV heads, hd 128, 4096 cached rows), through the C ABI: the
@@ -13,7 +13,7 @@ in HBM before the timed region.
 One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time),
 roofline of the decode op (the same HIP-event time on the arena's stream),
 the CPU oracle timed on this host, and the other configs' figures (prefill
-TFLOP/s, ragged decode, ViT, quantized GEMV) under "extra". --copy-bytes N adds one arena
+TFLOP/s, ragged decode, ViT, quantized GEMV and GEMM) under "extra". --copy-bytes N adds one arena
 copy of N bytes, the calibration dispatch for rocprofv3 --pmc FETCH_SIZE /
 WRITE_SIZE runs.
 """
@@ -42,6 +42,7 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
 # size; profiles/decode_c2_pmc_traffic.md has the runs and the factors.
 DECODE_TRAFFIC_BYTES = 18_419_688
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 matrix, TFLOP/s
+INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 matrix, TOP/s
 
 
 class Hip:
@@ -260,6 +261,40 @@ def bench_gemv(hip: Hip, reps: int):
     return out
 
 
+def bench_gemm(hip: Hip, reps: int, n: int = 512):
+    """syn_hip_matmul_q for a prompt chunk of n activation rows (the int8
+    matrix-core GEMM, activation quantizer included) on the Llama-3-8B
+    shapes. TOP/s = 2 n rows cols / time."""
+    out = {}
+    g = wl.rng(wl.SEED + 23)
+    for name, t, rows, cols in GEMV_SHAPES[:3]:
+        bs, ts = GEMV_BLOCK[t]
+        wbytes = rows * (cols // bs) * ts
+        act_bytes = int(lib().syn_hip_matmul_q_act_bytes(t, n, cols))
+        arena = Arena(capi.align(wbytes) + n * cols * 4 + act_bytes + n * rows * 4 + (4 << 20))
+        w_off = arena.put(g.integers(0, 256, size=wbytes, dtype=np.uint8))
+        x_off = arena.put(wl.normal(g, (n, cols)))
+        act_off = arena.alloc(act_bytes)
+        out_off = arena.alloc(n * rows * 4)
+        d = capi.MatmulQDesc(w_offset=w_off, x_offset=x_off, act_offset=act_off, bias_offset=capi.NO_OFFSET,
+                             out_offset=out_off, w_type=t, n=n, rows=rows, cols=cols)
+        L = lib()
+        check(L.syn_hip_matmul_q(arena.handle, ctypes.byref(d)))
+        arena.sync()
+        t0, t1 = hip.events(2)
+        hip.record(t0, arena.stream)
+        for _ in range(reps):
+            check(L.syn_hip_matmul_q(arena.handle, ctypes.byref(d)))
+        hip.record(t1, arena.stream)
+        ms = hip.ms(t0, t1) / reps
+        arena.close()
+        tops = 2.0 * n * rows * cols / (ms * 1e-3) / 1e12
+        out[name] = {"n": n, "rows": rows, "cols": cols, "us": round(ms * 1e3, 2), "tops": round(tops, 1),
+                     "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        log(f"gemm {name} n={n} {rows}x{cols}: {ms * 1e3:.1f} us, {tops:.0f} TOP/s")
+    return out
+
+
 def cpu_baseline(cfg: wl.Decode, budget_s: float):
     """The CPU oracle (oracle/liboracle.so, a port of the reference's
     attention()) timed on this host: full config-2 decode steps, threads over
@@ -295,7 +330,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="same as --only decode")
-    ap.add_argument("--only", choices=["decode", "prefill", "ragged", "vision", "gemv"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "ragged", "vision", "gemv", "gemm"], default=None,
                     help="run one configuration (no JSON line unless it is decode)")
     ap.add_argument("--copy-bytes", type=int, default=0, help="one arena copy of this many bytes (PMC calibration)")
     args = ap.parse_args()
@@ -340,6 +375,8 @@ def main() -> int:
         log(f"vision: {vms * 1e3:.1f} us, {extra['vision']['tflops']:.0f} TFLOP/s")
     if only in (None, "gemv"):
         extra["gemv_q"] = bench_gemv(hip, 400)
+    if only in (None, "gemm"):
+        extra["gemm_q"] = bench_gemm(hip, 20)
     if only not in (None, "decode"):
         return 0
 

@@ -40,7 +40,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 HIP_SOURCES = ["kv_append.hip", "decode.hip", "prefill.hip", "flash.hip", "generic.hip", "rope.hip", "ops.hip",
-               "quant.hip", "capi.hip"]
+               "quant.hip", "quant_gemm.hip", "capi.hip"]
 
 
 def _run(cmd: list[str], cwd: pathlib.Path | None = None) -> None:

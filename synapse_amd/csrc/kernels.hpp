@@ -150,7 +150,14 @@ uint64_t qtype_act_bytes(uint32_t t, uint32_t n, uint32_t cols);    // quantized
 // LDS a quantized matmul may take for its activation rows (an 8-wave
 // workgroup), and the activation rows one pass can carry (0: cols too long).
 constexpr uint32_t matmul_q_max_lds = 160 * 1024;
+// From this many activation rows on, the quantized product runs as a GEMM
+// on the int8 matrix cores instead of passes of the GEMV.
+constexpr uint32_t matmul_q_gemm_rows = 32;
 uint32_t matmul_q_rows_per_pass(uint32_t n, uint32_t cols);
+// The same product for many activation rows on the int8 matrix cores
+// (quantizes x into act first).
+hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
+                         uint32_t n, uint32_t rows, uint32_t cols, hipStream_t stream);
 hipError_t launch_matmul_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
                            uint32_t n, uint32_t rows, uint32_t cols, hipStream_t stream);
 hipError_t launch_embed_q(uint32_t t, const uint8_t* table, float* out, const embed_tokens& tk, uint32_t n,

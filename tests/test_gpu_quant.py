@@ -79,7 +79,8 @@ def test_matmul_q_matches_ggml_golden(arena, name):
 
 
 @pytest.mark.parametrize("t", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])
-@pytest.mark.parametrize("n,rows,cols", [(1, 300, 2048), (3, 67, 4096), (2, 5, 256), (5, 9, 512), (1, 6, 20480)])
+@pytest.mark.parametrize("n,rows,cols", [(1, 300, 2048), (3, 67, 4096), (2, 5, 256), (5, 9, 512), (1, 6, 20480),
+                                         (31, 20, 512)])
 def test_matmul_q_matches_host_blocks(arena, t, n, rows, cols):
     rng = np.random.default_rng(1000 * t + rows)
     raw = random_blocks(t, rows, cols, rng)
@@ -100,6 +101,32 @@ def test_matmul_q_matches_host_blocks(arena, t, n, rows, cols):
         want = np.array([qh.vec_dot(raw[o * per_row:(o + 1) * per_row], t, act_rows[r]) for o in range(rows)])
         assert np.all(np.abs(out[r] - bias - want) <= 1e-5 * np.maximum(scale, 1.0)), (t, r)
         assert np.all(np.abs(out[r] - bias - w_all @ xa) <= 1e-5 * np.maximum(scale, 1.0)), (t, r)
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("n,rows,cols", [(32, 37, 512), (70, 130, 2048), (64, 128, 4096), (33, 300, 256),
+                                         (129, 33, 768)])
+def test_matmul_q_gemm_matches_host(arena, t, n, rows, cols):
+    """From 32 activation rows on, the product runs on the int8 matrix cores;
+    the activation bytes stay ggml's bit for bit and every output is within
+    1e-5 of sum |w| |x^| of the exact product of the dequantized operands
+    (each block's integer sum is exact; only float association differs)."""
+    if cols % BLOCK[t][0]:
+        pytest.skip("cols not whole blocks")
+    rng = np.random.default_rng(7000 + 31 * t + n)
+    raw = random_blocks(t, rows, cols, rng)
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    x[3, :256] = 0.0  # an all-zero block
+    bias = rng.standard_normal(rows).astype(np.float32)
+    out, act = matmul_q(arena, raw, t, x, rows, cols, bias)
+    want_act = np.concatenate([qh.quantize_act(x[r], t) for r in range(n)])
+    assert np.array_equal(act, want_act)
+    w_all = qh.dequantize(raw, t).reshape(rows, cols).astype(np.float64)
+    xa = np.stack([qh.dequantize_act(a, qh.act_type(t)) for a in want_act.reshape(n, -1)]).astype(np.float64)
+    exact = xa @ w_all.T
+    scale = np.abs(xa) @ np.abs(w_all).T
+    err = np.abs(out.astype(np.float64) - bias - exact)
+    assert np.all(err <= 1e-5 * np.maximum(scale, 1.0)), float((err / np.maximum(scale, 1.0)).max())
 
 
 @pytest.mark.parametrize("t", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])

@@ -39,6 +39,9 @@ HIP_FLAGS = [
     # Packed-FP32 instructions stay off on this pool (wrong results seen).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# Per-source additions: the int8 GEMM's products feed vector work directly,
+# so their results go to VGPRs (no accumulator-register moves).
+SOURCE_FLAGS = {"quant_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIP_SOURCES = ["kv_append.hip", "decode.hip", "prefill.hip", "flash.hip", "generic.hip", "rope.hip", "ops.hip",
                "quant.hip", "quant_gemm.hip", "capi.hip"]
 
@@ -57,7 +60,7 @@ def build_library() -> pathlib.Path:
 
     def compile_one(src: str) -> pathlib.Path:
         obj = BUILD / (pathlib.Path(src).stem + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        _run([HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)])
         return obj
 
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(HIP_SOURCES))) as ex:

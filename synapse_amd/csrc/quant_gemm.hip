@@ -26,6 +26,11 @@
 
 #include "quant.hpp"
 
+// The quantizers above keep ggml's rounding (no contraction); the GEMM's
+// float combines below may fuse: they differ from ggml's gemv by float
+// association in any case.
+#pragma clang fp contract(fast)
+
 namespace syn {
 
 namespace {

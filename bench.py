@@ -10,8 +10,10 @@ distinct KV states (>= 512 MiB together, as a real model's 32 layers are),
 so K and V come from HBM, not the 256 MB Infinity Cache. Inputs are resident
 in HBM before the timed region.
 
-One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time),
-roofline of the decode op (the same HIP-event time on the arena's stream),
+One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time,
+steps called one by one through the C ABI; "extra" also has the same steps
+replayed from a HIP graph, which measures the same), roofline of the decode
+op (the same HIP-event time on the arena's stream),
 the CPU oracle timed on this host, and the other configs' figures (prefill
 TFLOP/s, ragged decode, ViT, quantized GEMV and GEMM) under "extra". --copy-bytes N adds one arena
 copy of N bytes, the calibration dispatch for rocprofv3 --pmc FETCH_SIZE /
@@ -103,9 +105,9 @@ def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int)
     for i in range(warmup):
         check(L.syn_hip_attention(arena.handle, ctypes.byref(descs[i % layers])))
     arena.sync()
-    # Timed region: whole steps back to back. A single-token step is one
-    # launch (the decode kernel appends the row itself), so this is also the
-    # decode kernel's average launch duration.
+    # Timed region: whole steps back to back, each called through the C ABI
+    # (two launches: the split kernel, which appends the row itself, and the
+    # merge kernel).
     t0, t1 = hip.events(2)
     hip.record(t0, stream)
     w0 = time.perf_counter()
@@ -124,9 +126,27 @@ def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int)
     kern = [hip.ms(evs[2 * i], evs[2 * i + 1]) for i in range(steps)]
     out = arena.download(descs[0].out_offset, (qsz,), np.float32)
     assert np.all(np.isfinite(out))
+    # The same steps replayed from a HIP graph: one graph holds one step per
+    # KV state (as a model's decode step holds one per layer), replayed until
+    # `steps` steps have run; one host call per graph instead of per step. It
+    # shows whether host launch overhead shapes the per-call figure.
+    byref = [ctypes.byref(d) for d in descs]
+    graph = capi.HipGraph(arena, lambda: [check(L.syn_hip_attention(arena.handle, r)) for r in byref])
+    reps = max(1, steps // layers)
+    for _ in range(2):
+        graph.launch()
+    arena.sync()
+    hip.record(t0, stream)
+    for _ in range(reps):
+        graph.launch()
+    hip.record(t1, stream)
+    graph_ms = hip.ms(t0, t1) / (reps * layers)
+    graph.close()
+    out_g = arena.download(descs[0].out_offset, (qsz,), np.float32)
+    assert np.array_equal(out_g.view(np.uint32), out.view(np.uint32))
     arena.close()
-    return step_ms, step_ms, {"wall_ms_per_step": wall_ms, "kernel_ms_median": float(np.median(kern)),
-                              "kernel_ms_mean_bracketed": float(np.mean(kern))}
+    return step_ms, graph_ms, {"wall_ms_per_step": wall_ms, "kernel_ms_median": float(np.median(kern)),
+                               "kernel_ms_mean_bracketed": float(np.mean(kern)), "graph_steps": reps * layers}
 
 
 def bench_prefill(hip: Hip, cfg: wl.Prefill, reps: int):
@@ -382,12 +402,15 @@ def main() -> int:
 
     cfg = wl.C2
     log(f"decode {cfg.name}: {args.steps} steps, {args.warmup} warmup, {args.layers} rotating KV states")
-    step_ms, kern_ms, det = bench_decode(hip, cfg, args.steps, args.warmup, args.layers)
+    step_ms, graph_ms, det = bench_decode(hip, cfg, args.steps, args.warmup, args.layers)
+    kern_ms = step_ms
     nbytes = cfg.kv_bytes()
     value = nbytes / (step_ms * 1e-3) / 1e9
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
-    log(f"decode: {step_ms * 1e3:.2f} us/step -> {value:.0f} GB/s")
+    log(f"decode: {step_ms * 1e3:.2f} us/step -> {value:.0f} GB/s "
+        f"({graph_ms * 1e3:.2f} us/step replayed from a HIP graph)")
     extra.update({"decode_step_us": round(step_ms * 1e3, 3),
+                  "decode_graph_step_us": round(graph_ms * 1e3, 3),
                   "decode_tokens_per_s_32_layers": round(1e3 / (step_ms * 32), 1),
                   "decode_wall_us_per_step": round(det["wall_ms_per_step"] * 1e3, 3),
                   "decode_single_step_us_median": round(det["kernel_ms_median"] * 1e3, 3),

@@ -149,6 +149,65 @@ def check(status: int) -> None:
         raise SynHipError(status, detail or lib().syn_hip_error_string(status).decode())
 
 
+class HipGraph:
+    """A HIP graph captured from the C ABI calls `record()` makes on an
+    arena's stream, replayed with `launch()`: for launch-bound loops (one
+    decode step per layer, say), whose kernels the graph replays with one
+    host call. Calls that allocate, synchronise or copy to the host cannot
+    be captured; the attention, RoPE and model-op entry points only launch
+    kernels on the arena's stream."""
+
+    _CAPTURE_RELAXED = 2  # hipStreamCaptureModeRelaxed
+
+    def __init__(self, arena: "Arena", record):
+        rt = _hip_runtime()
+        self._rt = rt
+        self.stream = ctypes.c_void_p(arena.stream)
+        graph = ctypes.c_void_p()
+        self._exec = ctypes.c_void_p()
+        _hip_ok(rt.hipStreamBeginCapture(self.stream, self._CAPTURE_RELAXED), "hipStreamBeginCapture")
+        try:
+            record()
+        finally:
+            _hip_ok(rt.hipStreamEndCapture(self.stream, ctypes.byref(graph)), "hipStreamEndCapture")
+        try:
+            _hip_ok(rt.hipGraphInstantiate(ctypes.byref(self._exec), graph, None, None, 0), "hipGraphInstantiate")
+        finally:
+            rt.hipGraphDestroy(graph)
+
+    def launch(self) -> None:
+        _hip_ok(self._rt.hipGraphLaunch(self._exec, self.stream), "hipGraphLaunch")
+
+    def close(self) -> None:
+        if self._exec:
+            self._rt.hipGraphExecDestroy(self._exec)
+            self._exec = ctypes.c_void_p()
+
+
+_rt = None
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    global _rt
+    if _rt is None:
+        rt = ctypes.CDLL("libamdhip64.so")
+        vp = ctypes.c_void_p
+        for name, args in {"hipStreamBeginCapture": [vp, ctypes.c_int],
+                           "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+                           "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t],
+                           "hipGraphLaunch": [vp, vp], "hipGraphDestroy": [vp],
+                           "hipGraphExecDestroy": [vp]}.items():
+            getattr(rt, name).argtypes = args
+            getattr(rt, name).restype = ctypes.c_int
+        _rt = rt
+    return _rt
+
+
+def _hip_ok(status: int, what: str) -> None:
+    if status != 0:
+        raise SynHipError(status, f"{what} failed with HIP error {status}")
+
+
 def align(x: int, a: int = 256) -> int:
     return (x + a - 1) // a * a
 

@@ -66,6 +66,14 @@ def test_decode_lengths_cross_split_edges(arena, ctx):
     assert_close(got, want, what=f"ctx {ctx}")
 
 
+@pytest.mark.parametrize("ctx", [70000, 150000])
+def test_decode_long_contexts(arena, ctx):
+    """Long caches take longer splits (512 and 1024 positions here, 137 and
+    147 splits), so the merge combines many partials."""
+    got, want, _, _ = _case(arena, 32, 8, 128, ctx, seed=7 + ctx, theta=500000.0)
+    assert_close(got, want, what=f"ctx {ctx}")
+
+
 @pytest.mark.parametrize("n_heads,n_kv,hd", [(8, 8, 32), (4, 2, 16), (16, 8, 64), (28, 4, 128), (32, 2, 128),
                                              (16, 1, 128), (8, 2, 80), (12, 4, 96), (8, 4, 256), (6, 3, 40)])
 def test_decode_head_layouts(arena, n_heads, n_kv, hd):

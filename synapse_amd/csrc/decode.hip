@@ -197,12 +197,20 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     // q^T operand: lane (G, r) holds head h0 + r, dims G*SPAN + 8*st + [0, 8),
     // rounded to binary16 as attend_group rounds q (S/kernels/attention.hpp:204-206).
     h8 qv[NS];
-    const auto convert_q = [&]() {
-        // Wait for q's copy only: the K, V loads issued after it stay in
-        // flight. Every wave has waited for its own copies, so the barrier
-        // needs no more than the LDS counter (__syncthreads() would also wait
-        // for the K, V loads).
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NS + NT));
+    const auto convert_q = [&](bool kv_issued) {
+        // Wait for this wave's copies (q, the new row) only: the K, V loads
+        // issued after them stay in flight. A wave with no positions issued
+        // none, so it waits for everything it has. Every wave has waited for
+        // its own copies, so the barrier needs no more than the LDS counter
+        // (__syncthreads() would also wait for the K, V loads). A batched
+        // launch waits for its first K, V too: it runs many blocks per CU,
+        // which hide the wait, and the schedule the early q then allows needs
+        // more registers than two blocks per SIMD pair leave.
+        if (kv_issued && !MULTI) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NS + NT));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
@@ -347,7 +355,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     if (tb < t_end) {
         load_kv(tb, kr, vr);
     }
-    convert_q();
+    convert_q(tb < t_end);
     while (tb < t_end) {
         step(tb, kr, vr);
         tb += stride;

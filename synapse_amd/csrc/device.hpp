@@ -39,12 +39,9 @@ __device__ __forceinline__ void store16(void* p, u4 v) {
     *reinterpret_cast<u4*>(p) = v;
 }
 
-// Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes at
-// g land at lds + 16 * l; lds must be the same for every lane of the wave.
-// Counted by vmcnt like any vector load, and takes no registers.
-__device__ __forceinline__ void load16_lds(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+// Byte address of an LDS location (what M0 and ds_* addresses take).
+__device__ __forceinline__ uint32_t lds_address(const void* lds) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)lds));
 }
 
 // Raw buffer access: a 128-bit resource (base, byte limit) in scalar
@@ -59,6 +56,28 @@ __device__ __forceinline__ rsrc make_rsrc(const void* base, uint32_t bytes) {
 }
 __device__ __forceinline__ u4 buffer_load16(rsrc r, uint32_t offset) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+}
+
+// Direct global -> LDS copies: lane l's 16 bytes land at lds + 16 * l; lds
+// must be the same for every lane of the wave. Counted by vmcnt like any
+// vector load, and they take no registers.
+//
+// They are issued through asm on purpose. The compiler cannot tell which LDS
+// bytes a copy writes, so after a copy it issued itself it waits for every
+// outstanding vector load (s_waitcnt vmcnt(0)) before the next LDS read of
+// any buffer: a pipeline's prefetch into one stage would then be waited for
+// before the other stage is read, and a decode block would wait for all its
+// K/V loads before reading q. Callers of these wait for their own copies
+// (s_waitcnt vmcnt(n), then an LDS-only barrier when other waves read them).
+// M0 holds the LDS address; one wait state separates its write from the copy.
+__device__ __forceinline__ void load16_lds(const void* g, void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_address(lds));
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(m0) : "memory");
+}
+// Lane l's 16 bytes at byte `offset` of r (zeros at or past its limit).
+__device__ __forceinline__ void buffer_load16_lds(rsrc r, void* lds, uint32_t offset) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_address(lds));
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(offset), "s"(r), "{m0}"(m0) : "memory");
 }
 
 // f32 -> binary16, round to nearest even (v_cvt_f16_f32 in the default mode),

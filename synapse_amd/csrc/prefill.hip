@@ -52,7 +52,7 @@ __device__ __forceinline__ void pf_barrier() {
 // One 1 KB tile copy: lane l's 16 bytes at byte `offset` of r land at
 // lds + 16 l (offsets at or past r's limit land as zeros).
 __device__ __forceinline__ void pf_copy(rsrc r, char* lds, uint32_t offset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, offset, 0, 0, 0);
+    buffer_load16_lds(r, lds, offset);
 }
 
 template <bool F16>
@@ -441,6 +441,11 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
                          ? pf_load_q<QF16>(a.q, static_cast<std::size_t>(my_q) * a.q_row + h * hd + d0)
                          : as_h8(zero_u4());
         }
+        // Wait for q here, once per query tile: left to the compiler, the
+        // wait would sit before every tile's first product (it cannot tell
+        // whether this ran) and hold each tile until the next tile's copy
+        // had landed too.
+        __builtin_amdgcn_s_waitcnt(pf_vmcnt(0));
     };
 
     // Copy offsets as in the 4-wave kernel, over the group's 4 waves; vc[i]
@@ -650,6 +655,8 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
     };
     // The group's pipeline over its items; both groups take `half` steps
     // (two barriers each), so every barrier has all 8 waves.
+    // The first query tile's q loads go out after the first two items'
+    // copies, and enter's wait covers all of them.
     const auto pipeline = [&](char* k0, char* v0, char* k1, char* v1) __attribute__((always_inline)) {
         if (cnt > 0) {
             issue(0, k0, v0);
@@ -657,7 +664,7 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
         if (cnt > 1) {
             issue(1, k1, v1);
         }
-        wait_item(cnt > 1);
+        enter(cur_qt);
         if (cnt > 0) {
             tail(0, v0);
         }
@@ -689,7 +696,6 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
         }
     };
     reset();
-    enter(cur_qt);
     if (grp == 0) {
         pipeline(lk00, lv00, lk01, lv01);
     } else {

@@ -80,6 +80,14 @@ __device__ __forceinline__ void buffer_load16_lds(rsrc r, void* lds, uint32_t of
     asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(offset), "s"(r), "{m0}"(m0) : "memory");
 }
 
+// Workgroup barrier that waits only for this wave's LDS operations.
+// __syncthreads() carries a release fence that also waits for every
+// outstanding vector load, prefetches meant to stay in flight across the
+// barrier included. The memory clobber keeps LDS accesses on their side.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // f32 -> binary16, round to nearest even (v_cvt_f16_f32 in the default mode),
 // the rounding kv_append and attend_group apply (S/numeric/half.hpp:46-82).
 __device__ __forceinline__ _Float16 to_h(float x) {

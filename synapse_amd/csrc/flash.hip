@@ -255,6 +255,26 @@ __host__ __device__ constexpr uint32_t resident_max_keys(uint32_t hdp) {
     }
     return np;
 }
+// Keys of the first staging half for np (padded) keys: about half, a
+// multiple of 64 (the compute steps' size), all of them up to 64.
+__host__ __device__ constexpr uint32_t resident_half1(uint32_t np) {
+    return np <= 64 ? np : (np / 128 > 0 ? np / 128 * 64 : 64);
+}
+// The most keys either half holds for up to npmax keys.
+__host__ __device__ constexpr uint32_t resident_half1_max(uint32_t npmax) {
+    uint32_t m = 0;
+    for (uint32_t np = 32; np <= npmax; np += 32) {
+        m = resident_half1(np) > m ? resident_half1(np) : m;
+    }
+    return m;
+}
+__host__ __device__ constexpr uint32_t resident_half2_max(uint32_t npmax) {
+    uint32_t m = 0;
+    for (uint32_t np = 32; np <= npmax; np += 32) {
+        m = np - resident_half1(np) > m ? np - resident_half1(np) : m;
+    }
+    return m;
+}
 
 template <int HD, bool F16>
 __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
@@ -280,13 +300,18 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
     char* lk = lds;
     char* lv = lds + np * KROWC * 16;
 
-    // ---- stage K rows and V^T (zeros past n and past hd) ----
-    // Every load of the block is issued before any LDS write, so staging
-    // costs one memory latency: CH chunks per thread at most (the largest n
-    // the resident form takes for this head size).
-    constexpr uint32_t CH = (resident_max_keys(HD) * KCPR + 255) / 256;
+    // ---- stage K rows and V^T in two halves of the keys ----
+    // Keys [0, kh) are the first half and [kh, np) the second. Every load of
+    // the block is issued at once, q and the first half first; the waves then
+    // run all their query tiles over the first half while the second half
+    // lands, and finish over the second. Zeros past n and past hd.
+    // f32 rows take twice the staging registers: they stage all keys at
+    // once (the first half is everything).
+    constexpr uint32_t NPMAX = resident_max_keys(HD);
+    constexpr uint32_t CH1 = ((F16 ? resident_half1_max(NPMAX) : NPMAX) * KCPR + 255) / 256;  // chunks per thread
+    constexpr uint32_t CH2 = F16 ? (resident_half2_max(NPMAX) * KCPR + 255) / 256 : 1;
     constexpr uint32_t ESZ = F16 ? 2 : 4;
-    const uint32_t nchunks = np * KCPR;
+    const uint32_t kh = F16 ? resident_half1(np) : np;
     // The image's rows through buffer resources: chunks past n or past hd
     // take an out-of-range offset and read as zeros, so every load is
     // unconditional.
@@ -304,9 +329,9 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
         }
     };
     // The wave's q tiles (wave (w + block) % 4 takes tiles w', w' + 4, ..., so
-    // the extra tiles of co-resident blocks land on different SIMDs) are
-    // loaded first, with the block's K and V: one memory latency for all.
-    constexpr uint32_t TPW = (resident_max_keys(HD) / 32 + 3) / 4;  // q tiles per wave, at most
+    // the extra tiles of co-resident blocks land on different SIMDs) go out
+    // first.
+    constexpr uint32_t TPW = (NPMAX / 32 + 3) / 4;  // q tiles per wave, at most
     const uint32_t n_qt = np / 32;
     const uint32_t w0 = (static_cast<uint32_t>(w) + blockIdx.x) % 4;
     const rsrc q_res = make_rsrc(static_cast<const char*>(a.q) + row_base * a.q_row * ESZ, n * a.q_row * ESZ);
@@ -320,51 +345,111 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
             qc[t][st] = chunk(q_res, my_q < n && d0 < hd ? (my_q * a.q_row + h * hd + d0) * ESZ : buffer_oob);
         }
     }
-    u4 kc[CH], vc[CH];
+    // Chunk i of a half [k0, k1): K takes row-major chunks (consecutive lanes
+    // read consecutive 16 bytes of a row), V takes consecutive keys of one
+    // 8-dim chunk (each of the 8 half-word writes of a wave then covers 128
+    // contiguous bytes of a V^T row).
+    const auto load_half = [&]<uint32_t C>(uint32_t k0, uint32_t k1, u4 (&kc)[C], u4 (&vc)[C])
+                               __attribute__((always_inline)) {
+        const uint32_t count = (k1 - k0) * KCPR, span = max(k1 - k0, 1u);  // an empty half loads nothing
 #pragma unroll
-    for (uint32_t i = 0; i < CH; ++i) {
-        const uint32_t idx = tid + 256 * i;
-        const uint32_t key = idx / KCPR, cc = idx % KCPR;
-        kc[i] = chunk(k_res, idx < nchunks && key < n && 8 * cc < hd ? (key * a.row + h * hd + 8 * cc) * ESZ
-                                                                      : buffer_oob);
-        // V: lanes take consecutive keys of one 8-dim chunk, so each of the
-        // 8 half-word writes of a wave covers 128 contiguous bytes of a V^T row.
-        const uint32_t vkey = idx % np, vcc = idx / np;
-        vc[i] = chunk(v_res, idx < nchunks && vkey < n && 8 * vcc < hd ? (vkey * a.row + h * hd + 8 * vcc) * ESZ
-                                                                         : buffer_oob);
-    }
+        for (uint32_t i = 0; i < C; ++i) {
+            const uint32_t idx = tid + 256 * i;
+            const uint32_t key = k0 + idx / KCPR, cc = idx % KCPR;
+            kc[i] = chunk(k_res, idx < count && key < n && 8 * cc < hd ? (key * a.row + h * hd + 8 * cc) * ESZ
+                                                                       : buffer_oob);
+            const uint32_t vkey = k0 + idx % span, vcc = idx / span;
+            vc[i] = chunk(v_res, idx < count && vkey < n && 8 * vcc < hd
+                                     ? (vkey * a.row + h * hd + 8 * vcc) * ESZ
+                                     : buffer_oob);
+        }
+    };
+    const auto store_half = [&]<uint32_t C>(uint32_t k0, uint32_t k1, const u4 (&kc)[C], const u4 (&vc)[C])
+                                __attribute__((always_inline)) {
+        const uint32_t count = (k1 - k0) * KCPR, span = max(k1 - k0, 1u);
 #pragma unroll
-    for (uint32_t i = 0; i < CH; ++i) {
-        const uint32_t idx = tid + 256 * i;
-        if (idx < nchunks) {
-            const uint32_t key = idx / KCPR, cc = idx % KCPR;
-            *reinterpret_cast<u4*>(lk + (key * KROWC + cc) * 16) = kc[i];
-            const uint32_t vkey = idx % np, vcc = idx / np;
-            const h8 hv = as_h8(vc[i]);
-            _Float16* col = reinterpret_cast<_Float16*>(lv) + (8 * vcc * vrowc * 8 + vkey);
+        for (uint32_t i = 0; i < C; ++i) {
+            const uint32_t idx = tid + 256 * i;
+            if (idx < count) {
+                const uint32_t key = k0 + idx / KCPR, cc = idx % KCPR;
+                *reinterpret_cast<u4*>(lk + (key * KROWC + cc) * 16) = kc[i];
+                const uint32_t vkey = k0 + idx % span, vcc = idx / span;
+                const h8 hv = as_h8(vc[i]);
+                _Float16* col = reinterpret_cast<_Float16*>(lv) + (8 * vcc * vrowc * 8 + vkey);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                col[j * vrowc * 8] = hv[j];
+                for (int j = 0; j < 8; ++j) {
+                    col[j * vrowc * 8] = hv[j];
+                }
             }
         }
+    };
+    u4 kc1[CH1], vc1[CH1], kc2[CH2], vc2[CH2];
+    load_half(0, kh, kc1, vc1);
+    if constexpr (F16) {
+        load_half(kh, np, kc2, vc2);
     }
-    // The V^T padding chunks are never read; the K padding chunk neither.
-    __syncthreads();
 
     // ---- the wave's query tiles over the resident keys ----
+    // The first tile runs over the first half while the second half lands;
+    // the other tiles start once all keys are resident.
+    f16v o[NT];
+    float m_run = -INFINITY, l_run = 0.0f;
+    h8 qv[NS];
+    // E 32-key slices from key t0 (keys past n masked).
+    const auto step = [&]<int E>(uint32_t t0) __attribute__((always_inline)) {
+        f16v sc[E];
 #pragma unroll
-    for (uint32_t tq = 0; tq < TPW; ++tq) {
-        const uint32_t qt = w0 + 4 * tq;
-        if (qt >= n_qt) {
-            break;
+        for (int e = 0; e < E; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                sc[e][i] = 0.0f;
+            }
+            const char* krow = lk + ((t0 + 32 * e + slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
+            }
         }
-        const uint32_t my_q = 32 * qt + qi;
-        h8 qv[NS];
+        // Register i of slice e holds key t0 + 32e + 16(i/8) + 8H + i%8:
+        // masked unless ck = 32e + 16(i/8) + i%8 < n - t0 - 8H.
+        if (t0 + 32 * E > n) {
+            const int dk = static_cast<int>(n - t0) - 8 * H;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int ck = 32 * e + 16 * (i >> 3) + (i & 7);
+                    sc[e][i] = ck < dk ? sc[e][i] : -INFINITY;
+                }
+            }
+        }
+        h8 pv[2 * E];
+        online_softmax<E, NT>(sc, c, m_run, l_run, o, pv);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            // V^T row 32t + qi, keys t0 + 8H + 16 s ..
+            const char* vrow = lv + ((32 * t + qi) * vrowc + t0 / 8 + H) * 16;
+#pragma unroll
+            for (int s2 = 0; s2 < 2 * E; ++s2) {
+                o[t] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[t]);
+            }
+        }
+    };
+    // Keys [k0, k1) of the current tile (k0 a multiple of 64).
+    const auto sweep = [&](uint32_t k0, uint32_t k1) __attribute__((always_inline)) {
+        uint32_t t0 = k0;
+        for (; t0 + 64 <= k1; t0 += 64) {
+            step.template operator()<2>(t0);
+        }
+        if (t0 < k1) {
+            step.template operator()<1>(t0);
+        }
+    };
+    const auto begin_tile = [&](uint32_t tq) __attribute__((always_inline)) {
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             qv[st] = as_h8(qc[tq][st]);
         }
-        f16v o[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -372,69 +457,55 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
                 o[t][i] = 0.0f;
             }
         }
-        float m_run = -INFINITY, l_run = 0.0f;
-        // E 32-key slices from key t0 (keys past n masked).
-        const auto step = [&]<int E>(uint32_t t0) __attribute__((always_inline)) {
-            f16v sc[E];
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    sc[e][i] = 0.0f;
-                }
-                const char* krow = lk + ((t0 + 32 * e + slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
-#pragma unroll
-                for (int st = 0; st < NS; ++st) {
-                    sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
-                }
-            }
-            // Register i of slice e holds key t0 + 32e + 16(i/8) + 8H + i%8.
-            if (t0 + 32 * E > n) {
-                const uint32_t lim = n - t0;
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const uint32_t kk = 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
-                        sc[e][i] = kk < lim ? sc[e][i] : -INFINITY;
-                    }
-                }
-            }
-            h8 pv[2 * E];
-            online_softmax<E, NT>(sc, c, m_run, l_run, o, pv);
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                // V^T row 32t + qi, keys t0 + 8H + 16 s ..
-                const char* vrow = lv + ((32 * t + qi) * vrowc + t0 / 8 + H) * 16;
-#pragma unroll
-                for (int s2 = 0; s2 < 2 * E; ++s2) {
-                    o[t] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[t]);
-                }
-            }
-        };
-        uint32_t t0 = 0;
-        for (; t0 + 64 <= np; t0 += 64) {
-            step.template operator()<2>(t0);
+        m_run = -INFINITY;
+        l_run = 0.0f;
+    };
+    const auto end_tile = [&](uint32_t tq) __attribute__((always_inline)) {
+        const uint32_t my_q = 32 * (w0 + 4 * tq) + qi;
+        if (my_q >= n) {
+            return;
         }
-        if (t0 < np) {
-            step.template operator()<1>(t0);
-        }
-        if (my_q < n) {
-            const float inv = 1.0f / l_run;
-            float* out = a.out + (row_base + my_q) * a.q_row + h * hd;
-            // Register i of tile t holds dim 32t + 8(i/4) + 4H + i%4.
+        const float inv = 1.0f / l_run;
+        float* out = a.out + (row_base + my_q) * a.q_row + h * hd;
+        // Register i of tile t holds dim 32t + 8(i/4) + 4H + i%4.
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
+        for (int t = 0; t < NT; ++t) {
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const uint32_t d = 32 * t + 8 * b + 4 * H;
-                    if (d < hd) {
-                        *reinterpret_cast<f4*>(out + d) = f4{o[t][4 * b] * inv, o[t][4 * b + 1] * inv,
-                                                             o[t][4 * b + 2] * inv, o[t][4 * b + 3] * inv};
-                    }
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t d = 32 * t + 8 * b + 4 * H;
+                if (d < hd) {
+                    *reinterpret_cast<f4*>(out + d) =
+                        f4{o[t][4 * b] * inv, o[t][4 * b + 1] * inv, o[t][4 * b + 2] * inv, o[t][4 * b + 3] * inv};
                 }
             }
         }
+    };
+    // LDS-only barriers: the second half's loads stay in flight across the
+    // first. No wave still reads the first half's rows when another writes
+    // the second half's: the halves are disjoint in LDS.
+    const bool first = w0 < n_qt;  // this wave has a tile at all
+    store_half(0, kh, kc1, vc1);
+    lds_barrier();
+    if (first) {
+        begin_tile(0);
+        sweep(0, kh);
+    }
+    if constexpr (F16) {
+        store_half(kh, np, kc2, vc2);
+        lds_barrier();
+    }
+    if (first) {
+        sweep(kh, np);
+        end_tile(0);
+    }
+#pragma unroll
+    for (uint32_t tq = 1; tq < TPW; ++tq) {
+        if (w0 + 4 * tq >= n_qt) {
+            break;
+        }
+        begin_tile(tq);
+        sweep(0, np);
+        end_tile(tq);
     }
 }
 

@@ -55,10 +55,15 @@ def test_vision_shapes_f32_inputs(arena, n, hd):
     _vision(arena, n, 2, 3, hd, SYN_F32)
 
 
-@pytest.mark.parametrize("n,hd", [(257, 64), (577, 64), (100, 128)])
+@pytest.mark.parametrize("n,hd", [(257, 64), (577, 64), (100, 128), (1, 64), (33, 32), (64, 64), (65, 64),
+                                  (96, 96), (190, 96), (128, 128), (288, 64), (540, 32)])
 def test_vision_many_heads_f16(arena, n, hd):
     """Several images and heads at once with f16 inputs: every (image, head)
-    block of the grid is checked."""
+    block of the grid is checked. With keys resident, f16 rows are staged in
+    two halves (the first query tile runs over the first while the second
+    lands): the shapes cover no second half (n <= 64), a second half ending
+    in a lone 32-key slice (65, 96, 257) and the largest resident n per head
+    size."""
     _vision(arena, n, 3, 5, hd, SYN_F16, seed=11)
 
 

@@ -205,13 +205,13 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
         // (__syncthreads() would also wait for the K, V loads). A batched
         // launch waits for its first K, V too: it runs many blocks per CU,
         // which hide the wait, and the schedule the early q then allows needs
-        // more registers than two blocks per SIMD pair leave.
+        // more registers than two waves per SIMD leave.
         if (kv_issued && !MULTI) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NS + NT));
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        lds_barrier();
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             const uint32_t d0 = G * SPAN + 8 * st;

@@ -38,15 +38,13 @@ constexpr int pf_vmcnt(int n) {
     return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
-// Workgroup barrier for the tile pipeline. __syncthreads() carries a release
-// fence that waits for every outstanding vector memory operation, the tile
-// copy just issued for the other stage included; here each wave waits for
-// its own copies with s_waitcnt vmcnt before this barrier, so the barrier only
-// needs the LDS operations (reads of the stage about to be refilled, the tail
-// fix-up writes) complete. The asm's memory clobber keeps the compiler from
-// moving LDS accesses across it.
+// Workgroup barrier for the tile pipeline: each wave waits for its own
+// copies with s_waitcnt vmcnt before it, so the barrier only needs the LDS
+// operations (reads of the stage about to be refilled, the tail fix-up
+// writes) complete, and the copy just issued for the other stage stays in
+// flight.
 __device__ __forceinline__ void pf_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    lds_barrier();
 }
 
 // One 1 KB tile copy: lane l's 16 bytes at byte `offset` of r land at

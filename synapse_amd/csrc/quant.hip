@@ -295,9 +295,8 @@ __global__ __launch_bounds__(512) void gemv_q_kernel(const uint8_t* w, const flo
         fetch_item(0, 0);
         fetch_item(1, 1);
     }
-    // LDS complete; the weight loads stay in flight (a __syncthreads() would
-    // wait for every outstanding memory operation).
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // LDS complete; the weight loads stay in flight.
+    lds_barrier();
 
     float acc[NR];
 #pragma unroll

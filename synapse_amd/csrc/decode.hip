@@ -111,12 +111,17 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
 
     // Block -> (sequence, split, KV head). Splits of one KV head are n_kv
     // blocks apart, so with n_kv a multiple of 8 they share an XCD (and its L2).
+    // A sequence's splits go out last first: the last split is the short one
+    // and holds the step's new row, and blocks dispatched last get their
+    // loads served last, so it must not be among them (measured: 0.9 us per
+    // config-2 step). Partials sit at the split's own slot.
     const uint32_t b = blockIdx.x;
     const uint32_t g = b % a.n_kv;
     const uint32_t sb = b / a.n_kv;
     const uint32_t si = find_seq<MULTI>(a.block0s, a.n_seqs, sb);
     const decode_seq& s = a.seq[si];
-    const uint32_t split = sb - s.block0;
+    const uint32_t split = s.n_splits - 1 - (sb - s.block0);
+    const std::size_t slot = static_cast<std::size_t>(s.block0 + split) * a.n_kv + g;
     const uint32_t t_begin = split * a.chunk;
     const uint32_t t_end = min(s.len, t_begin + a.chunk);
     const uint32_t h0 = g * group;
@@ -409,10 +414,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
             s.out[static_cast<std::size_t>(h0) * hd + e] = acc / sum;
         } else {
             // This split's partial; the merge kernel combines them.
-            a.part_o[static_cast<std::size_t>(b) * nout + e] = acc;
+            a.part_o[slot * nout + e] = acc;
             if (d == 0) {
-                a.part_ml[(static_cast<std::size_t>(b) * group + h) * 2] = mx;
-                a.part_ml[(static_cast<std::size_t>(b) * group + h) * 2 + 1] = sum;
+                a.part_ml[(slot * group + h) * 2] = mx;
+                a.part_ml[(slot * group + h) * 2 + 1] = sum;
             }
         }
     }

@@ -170,8 +170,18 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     _Float16* kbase = s.k + g * hd + G * SPAN;
     const uint32_t row2 = a.row * 2;
     const uint32_t vstride2 = s.ctx_stride * 2;
+    // The new row's own cache slot is not read (the step overwrites it), nor
+    // are V columns that start at or past it or the split end: those lanes
+    // take zeros and send no request, so a split holding only the new row
+    // waits for no memory. k_rows counts the rows read. K leaves the rest out
+    // through the resource's limit; a V column offset moved past the limit
+    // may wrap into the buffer, which reads valid memory whose values the
+    // step then replaces or zeroes.
+    // (readfirstlane: without it the batched kernel cannot tell the limit is
+    // uniform and wraps every K load in a loop over lanes.)
+    const uint32_t k_rows = __builtin_amdgcn_readfirstlane(min(t_end, s.len - (s.k_new != nullptr ? 1u : 0u)) - t_begin);
     const rsrc k_res = make_rsrc(s.k + static_cast<std::size_t>(t_begin) * a.row + g * hd,
-                                 (t_end - t_begin) * row2 - g * hd * 2);
+                                 k_rows ? k_rows * row2 - g * hd * 2 : 0u);
     const rsrc v_res = make_rsrc(s.vt + static_cast<std::size_t>(g) * hd * s.ctx_stride + t_begin,
                                  hd * vstride2 - t_begin * 2);
     const auto load_kv = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
@@ -184,7 +194,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
                 kr[e][st] = buffer_load16(k_res, d0 < hd ? rel * row2 + d0 * 2 : buffer_oob);
             }
         }
-        const uint32_t rel_v = (tb - t_begin + 8 * G) * 2;
+        const uint32_t rel_t = tb - t_begin + 8 * G;
+        const uint32_t rel_v = rel_t < k_rows ? rel_t * 2 : buffer_oob;
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
             const uint32_t dim = 16 * n + r;

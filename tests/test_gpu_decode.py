@@ -130,6 +130,37 @@ def test_decode_gqa_growing_cache(arena):
             assert np.max(np.abs(got[0, h * hd:(h + 1) * hd] - ref)) < 2e-3
 
 
+@pytest.mark.parametrize("ctx", [0, 1, 31, 127, 128, 129, 4000, 4096])
+def test_decode_ignores_slots_from_the_new_row_on(arena, ctx):
+    """Every cache slot from the step's position on holds NaN before the step,
+    K rows and V^T columns up to the row stride alike. The kernel must read
+    none of them: the new row's slot is overwritten by the step, the rest lie
+    past the sequence."""
+    n_heads, n_kv, hd = 32, 8, 128
+    cfg = wl.Decode("case", n_heads, n_kv, hd, ctx, 500000.0)
+    kc, vc, q, k, v = wl.decode_inputs(cfg, seed=60 + ctx)
+    max_ctx = ctx + 40
+    mark = arena.top
+    cache = capi.kv_state(arena, max_ctx, n_kv, hd)
+    nan16 = np.uint16(0x7E00)
+    kfull = np.full((max_ctx, n_kv * hd), nan16, dtype=np.uint16)
+    kfull[:ctx] = kc
+    arena.upload(cache.k_offset, kfull)
+    vt = np.full((n_kv * hd, cache.ctx_stride), nan16, dtype=np.uint16)
+    vt[:, :ctx] = vc.T
+    arena.upload(cache.v_offset, vt)
+    scratch = scratch_for(arena, n_heads, n_kv, hd, max_ctx)
+    got = attention(arena, cache, scratch, q, k, v, ctx, n_heads, cfg.scale)
+    dk, dv = capi.download_cache(arena, cache, ctx + 1)
+    arena.top = mark
+    ok_k, ok_v = orc.new_cache(ctx + 1, n_kv, hd)
+    ok_k[:ctx], ok_v[:ctx] = kc, vc
+    want = orc.attention_rows(q, k, v, ctx, ok_k, ok_v, n_heads, cfg.scale)
+    assert np.isfinite(got).all()
+    assert np.array_equal(dk[ctx], ok_k[ctx]) and np.array_equal(dv[ctx], ok_v[ctx])
+    assert_close(got, want, what=f"NaN past ctx {ctx}")
+
+
 def test_decode_is_deterministic(arena):
     """Fixed split count and merge order: two runs agree bit for bit."""
     a, _, _, _ = _case(arena, 32, 8, 128, 6000, seed=5)

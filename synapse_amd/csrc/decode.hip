@@ -445,9 +445,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const decode_args a) 
     const uint32_t u = blockIdx.x;
     const uint32_t si = find_seq<MULTI>(a.merge0s, a.n_seqs, u);
     const decode_seq& s = a.seq[si];
+    // Heads of one KV head go n_kv blocks apart, as the split kernel's
+    // blocks do, so with n_kv a multiple of 8 a merge block runs on the XCD
+    // whose L2 took its KV head's partials.
     const uint32_t k = u - s.merge0;
-    const uint32_t g = k / a.group;
-    const uint32_t h = k % a.group;
+    const uint32_t g = k % a.n_kv;
+    const uint32_t h = k / a.n_kv;
     const uint32_t hd = a.hd;
     const uint32_t nout = a.group * hd;
     const uint32_t S = s.n_splits;

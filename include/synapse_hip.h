@@ -233,7 +233,7 @@ typedef struct syn_norm_desc {
     uint64_t out_offset;    /* n rows of size f32; may alias in */
     uint32_t n;
     uint32_t size;
-    float eps;              /* > 0 */
+    float eps;              /* >= 0 */
     uint32_t reserved;
 } syn_norm_desc;
 
@@ -280,8 +280,9 @@ int syn_hip_matmul_q(syn_arena* arena, const syn_matmul_q_desc* desc);
  * SYN_ADD a + b (op_add, and op_add_rows over whole tables), SYN_MUL a * b
  * (op_mul), SYN_SILU_MUL silu(a) * b (op_silu then op_mul), SYN_SCALE
  * a * scalar (kernels::scale, as op_attn_temperature applies it), SYN_GELU
- * gelu(a) in ggml's binary16-rounded form (op_gelu). out may alias a or b. */
-enum { SYN_ADD = 0, SYN_MUL = 1, SYN_SILU_MUL = 2, SYN_SCALE = 3, SYN_GELU = 4 };
+ * gelu(a) in ggml's binary16-rounded form (op_gelu), SYN_SILU
+ * a / (1 + exp(-a)) (op_silu). out may alias a or b. */
+enum { SYN_ADD = 0, SYN_MUL = 1, SYN_SILU_MUL = 2, SYN_SCALE = 3, SYN_GELU = 4, SYN_SILU = 5 };
 
 typedef struct syn_elementwise_desc {
     uint64_t a_offset;
@@ -294,6 +295,18 @@ typedef struct syn_elementwise_desc {
 
 int syn_hip_elementwise(syn_arena* arena, const syn_elementwise_desc* desc);
 
+/* Softmax per row: out = exp(x - max) * float(1 / sum), the sum in double.
+ * Replaces execute(const op_softmax&), S/graph/session.hpp:319-323
+ * (kernels::softmax, S/kernels/elementwise.hpp:169-199). */
+typedef struct syn_softmax_desc {
+    uint64_t in_offset;  /* n rows of size f32 */
+    uint64_t out_offset; /* n rows of size f32; may alias in */
+    uint32_t n;
+    uint32_t size;       /* >= 1 */
+} syn_softmax_desc;
+
+int syn_hip_softmax(syn_arena* arena, const syn_softmax_desc* desc);
+
 /* Layer norm per row: ((x - mean) / sqrt(var + eps)) * gamma + beta, sums in
  * double. Replaces execute(const op_layer_norm&), S/graph/session.hpp:380-392
  * (kernels::layer_norm, S/kernels/elementwise.hpp:240-305). */
@@ -304,7 +317,7 @@ typedef struct syn_layer_norm_desc {
     uint64_t out_offset;    /* n rows of size f32; may alias in */
     uint32_t n;
     uint32_t size;
-    float eps;              /* > 0 */
+    float eps;              /* >= 0 */
     uint32_t reserved;
 } syn_layer_norm_desc;
 

@@ -82,6 +82,7 @@ CPP_TESTS = {
     # name: (source, links the CPU oracle)
     "test_graph": ("tests/cpp/test_graph.cpp", False),
     "test_session": ("tests/cpp/test_session.cpp", True),
+    "test_model_session": ("tests/cpp/test_model_session.cpp", False),
 }
 
 

@@ -82,7 +82,11 @@ class PixelShuffleDesc(ctypes.Structure):
                 ("scale", u32)]
 
 
-SYN_ADD, SYN_MUL, SYN_SILU_MUL, SYN_SCALE, SYN_GELU = 0, 1, 2, 3, 4
+class SoftmaxDesc(ctypes.Structure):
+    _fields_ = [("in_offset", u64), ("out_offset", u64), ("n", u32), ("size", u32)]
+
+
+SYN_ADD, SYN_MUL, SYN_SILU_MUL, SYN_SCALE, SYN_GELU, SYN_SILU = 0, 1, 2, 3, 4, 5
 
 
 # name -> (restype, argtypes); every symbol include/synapse_hip.h declares.
@@ -114,6 +118,7 @@ SIGNATURES = {
     "syn_hip_elementwise": (i32, [ctypes.c_void_p, ctypes.POINTER(ElementwiseDesc)]),
     "syn_hip_matmul_q_act_bytes": (u64, [u32, u32, u32]),
     "syn_hip_matmul_q": (i32, [ctypes.c_void_p, ctypes.POINTER(MatmulQDesc)]),
+    "syn_hip_softmax": (i32, [ctypes.c_void_p, ctypes.POINTER(SoftmaxDesc)]),
     "syn_hip_layer_norm": (i32, [ctypes.c_void_p, ctypes.POINTER(LayerNormDesc)]),
     "syn_hip_pixel_shuffle": (i32, [ctypes.c_void_p, ctypes.POINTER(PixelShuffleDesc)]),
 }

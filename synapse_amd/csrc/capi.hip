@@ -781,7 +781,7 @@ int syn_hip_rms_norm(syn_arena* a, const syn_norm_desc* d) {
     if (d == nullptr) {
         return fail(SYN_HIP_EINVAL, "null descriptor");
     }
-    if (d->size == 0 || !(std::isfinite(d->eps) && d->eps > 0.0f)) {
+    if (d->size == 0 || !(std::isfinite(d->eps) && d->eps >= 0.0f)) {
         return fail(SYN_HIP_EINVAL, "rms_norm: size %u, eps %g", d->size, static_cast<double>(d->eps));
     }
     if (d->n == 0) {
@@ -920,7 +920,7 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
     if (d == nullptr) {
         return fail(SYN_HIP_EINVAL, "null descriptor");
     }
-    if (d->op > SYN_GELU) {
+    if (d->op > SYN_SILU) {
         return fail(SYN_HIP_EINVAL, "elementwise: op %u", d->op);
     }
     if (d->count == 0) {
@@ -937,7 +937,7 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
         return e;
     }
     const float* b = nullptr;
-    if (d->op != SYN_SCALE && d->op != SYN_GELU) {
+    if (d->op != SYN_SCALE && d->op != SYN_GELU && d->op != SYN_SILU) {
         if (int e = check_range(a, d->b_offset, bytes, 4, "elementwise b")) {
             return e;
         }
@@ -949,6 +949,35 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
                       "elementwise launch");
 }
 
+int syn_hip_softmax(syn_arena* a, const syn_softmax_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->size == 0) {
+        return fail(SYN_HIP_EINVAL, "softmax: size 0");
+    }
+    if (d->n == 0) {
+        return SYN_HIP_OK;
+    }
+    const uint64_t bytes = uint64_t{d->n} * d->size * 4;
+    if (int e = check_range(a, d->in_offset, bytes, 4, "softmax in")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, bytes, 4, "softmax out")) {
+        return e;
+    }
+    if (d->in_offset != d->out_offset && d->in_offset < d->out_offset + bytes && d->out_offset < d->in_offset + bytes) {
+        return fail(SYN_HIP_EINVAL, "softmax: out overlaps in without being it");
+    }
+    return hip_status(syn::launch_softmax(reinterpret_cast<const float*>(a->base + d->in_offset),
+                                          reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->size,
+                                          a->stream),
+                      "softmax launch");
+}
+
 int syn_hip_layer_norm(syn_arena* a, const syn_layer_norm_desc* d) {
     if (int e = check_arena(a)) {
         return e;
@@ -956,7 +985,7 @@ int syn_hip_layer_norm(syn_arena* a, const syn_layer_norm_desc* d) {
     if (d == nullptr) {
         return fail(SYN_HIP_EINVAL, "null descriptor");
     }
-    if (d->size == 0 || !(std::isfinite(d->eps) && d->eps > 0.0f)) {
+    if (d->size == 0 || !(std::isfinite(d->eps) && d->eps >= 0.0f)) {
         return fail(SYN_HIP_EINVAL, "layer_norm: size %u, eps %g", d->size, static_cast<double>(d->eps));
     }
     if (d->n == 0) {

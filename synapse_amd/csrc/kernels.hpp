@@ -132,9 +132,11 @@ enum elementwise_op : uint32_t {
     elementwise_silu_mul = 2,  // silu(a) * b
     elementwise_scale = 3,     // a * scalar
     elementwise_gelu = 4,      // gelu(a), ggml's binary16-rounded tanh form
+    elementwise_silu = 5,      // silu(a)
 };
 hipError_t launch_embed(const float* table, float* out, const embed_tokens& t, uint32_t n, uint32_t size,
                         hipStream_t stream);
+hipError_t launch_softmax(const float* in, float* out, uint32_t n, uint32_t size, hipStream_t stream);
 hipError_t launch_rms_norm(const float* in, const float* gamma, float* out, uint32_t n, uint32_t size, float eps,
                            hipStream_t stream);
 hipError_t launch_matmul(const float* w, const float* x, const float* bias, float* out, uint32_t n, uint32_t rows,

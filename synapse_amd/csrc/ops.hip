@@ -119,11 +119,57 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const float* a, const 
         case elementwise_gelu:
             y = gelu_f16_table(x);
             break;
+        case elementwise_silu:  // kernels::silu
+            y = x / (1.0f + expf(-x));
+            break;
         default:  // elementwise_scale
             y = x * scalar;
             break;
         }
         out[e] = y;
+    }
+}
+
+// Row softmax (kernels::softmax, S/kernels/elementwise.hpp:169-199): the row
+// maximum subtracted before expf, the exponentials summed in double, and
+// every one multiplied by the float of 1 / sum. One block per row; out may
+// alias in (each element is read before it is written, by the same thread).
+__global__ __launch_bounds__(256) void softmax_kernel(const float* in, float* out, uint32_t size) {
+    __shared__ float wmax[4];
+    __shared__ double wsum[4];
+    const float* x = in + static_cast<std::size_t>(blockIdx.x) * size;
+    float* y = out + static_cast<std::size_t>(blockIdx.x) * size;
+    const int w = threadIdx.x >> 6;
+    float m = -INFINITY;
+    for (uint32_t i = threadIdx.x; i < size; i += 256) {
+        m = fmaxf(m, x[i]);
+    }
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, k, wave));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        wmax[w] = m;
+    }
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    double s = 0.0;
+    for (uint32_t i = threadIdx.x; i < size; i += 256) {
+        const float e = expf(x[i] - m);
+        y[i] = e;
+        s += e;
+    }
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) {
+        s += __shfl_xor(s, k, wave);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        wsum[w] = s;
+    }
+    __syncthreads();
+    const float scale = static_cast<float>(1.0 / (((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]));
+    for (uint32_t i = threadIdx.x; i < size; i += 256) {
+        y[i] *= scale;
     }
 }
 
@@ -202,6 +248,11 @@ hipError_t launch_embed(const float* table, float* out, const embed_tokens& t, u
                         hipStream_t stream) {
     const dim3 grid(grid_for(size), n);
     embed_kernel<<<grid, 256, 0, stream>>>(table, out, t, size);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(const float* in, float* out, uint32_t n, uint32_t size, hipStream_t stream) {
+    softmax_kernel<<<n, 256, 0, stream>>>(in, out, size);
     return hipGetLastError();
 }
 

@@ -3,25 +3,28 @@
 // 82-467) owns a host arena laid out by the static plan plus the KV states;
 // this one owns a device arena laid out the same way:
 //
-//   [ planned tensors: plan(g), 256-byte aligned ][ RoPE frequency tables ]
-//   [ KV state 0 ][ KV state 1 ] ...   (each syn_hip_kv_state_bytes, aligned)
+//   [ planned tensors: plan(g), 256-byte aligned ][ bound weights ]
+//   [ RoPE frequency tables ][ KV state 0 ][ KV state 1 ] ...
 //
-// one syn_hip_arena_create at construction and nothing allocated afterwards.
-// run(batch) keeps the reference's contract (S/graph/session.hpp:143-177):
-// it returns false and runs nothing unless 1 <= n <= max_batch and
-// pos + n <= position_limit; otherwise it executes every node in graph order
-// on the arena's stream -- op_rope through syn_hip_rope, op_attention through
-// syn_hip_attention (the drop-in for execute(op_attention), :348-374) and
-// op_self_attention through syn_hip_self_attention (execute(op_self_attention),
-// :409-449). Inputs are written and outputs read with write()/read(), the
-// device counterparts of tensor(t) (:107-110). A HIP failure during a run
-// stops it, returns false and is kept in status().
+// one syn_hip_arena_create at construction, which also copies every matrix
+// the graph binds (each distinct host matrix once), and nothing allocated
+// afterwards. run(batch) keeps the reference's contract (:143-177): it
+// returns false and runs nothing unless 1 <= n <= max_batch (n == max_batch
+// for a pixel-shuffle graph), pos + n <= position_limit and every token <
+// token_limit; otherwise it executes every node in graph order on the
+// arena's stream, each through its C-ABI call (execute(op_*), :287-453).
+// Inputs are written and outputs read with write()/read(), the device
+// counterparts of tensor(t) (:107-110). A HIP failure during a run stops
+// it, returns false and is kept in status().
 #pragma once
 
 #include "graph.hpp"
 #include "planner.hpp"
 
+#include <array>
+#include <cmath>
 #include <span>
+#include <unordered_map>
 
 namespace syn::graph {
 
@@ -40,6 +43,26 @@ public:
     explicit session(const compute_graph& g) : graph_(&g), plan_(plan(g)) {
         std::size_t top = plan_.arena_bytes;
         const auto& nodes = g.nodes();
+        // Every bound matrix once, keyed by its host data.
+        std::unordered_map<const void*, std::uint64_t> placed;
+        std::vector<std::pair<std::uint64_t, const matrix_ref*>> uploads;
+        weight_offset_.assign(nodes.size(), {no_offset, no_offset});
+        for (std::size_t i = 0; i < nodes.size(); ++i) {
+            const auto bound = bound_matrices(nodes[i]);
+            for (std::size_t j = 0; j < bound.size(); ++j) {
+                const matrix_ref* m = bound[j];
+                if (m == nullptr || std::holds_alternative<std::monostate>(*m)) {
+                    continue;
+                }
+                const void* key = std::get<weight_view>(*m).data;
+                auto [it, fresh] = placed.try_emplace(key, top);
+                if (fresh) {
+                    uploads.emplace_back(top, m);
+                    top = align_up(top + matrix_bytes(*m));
+                }
+                weight_offset_[i][j] = it->second;
+            }
+        }
         const_offset_.assign(nodes.size(), ~std::uint64_t{0});
         for (std::size_t i = 0; i < nodes.size(); ++i) {
             if (const auto* r = std::get_if<op_rope>(&nodes[i]); r && !r->freq_factors.empty()) {
@@ -61,6 +84,11 @@ public:
         if (status_ != SYN_HIP_OK) {
             arena_ = nullptr;
             return;
+        }
+        for (const auto& [offset, m] : uploads) {
+            if (status_ == SYN_HIP_OK) {
+                status_ = syn_hip_upload(arena_, offset, std::get<weight_view>(*m).data, matrix_bytes(*m));
+            }
         }
         for (std::size_t i = 0; i < nodes.size() && status_ == SYN_HIP_OK; ++i) {
             if (const_offset_[i] != ~std::uint64_t{0}) {
@@ -129,12 +157,19 @@ public:
         if (!accepts(n, b.pos)) {
             return false;
         }
+        for (std::uint32_t t : b.tokens) {
+            if (t >= graph_->token_limit()) {
+                return false;
+            }
+        }
+        tokens_ = b.tokens.data();
         return execute_all(n, 1, b.pos);
     }
 
-    // n rows at position 0, one image (S/graph/session.hpp:164-171).
+    // n rows at position 0, one image, for a graph that embeds nothing
+    // (S/graph/session.hpp:164-171).
     [[nodiscard]] bool run_rows(std::size_t n) noexcept {
-        if (!accepts(n, 0)) {
+        if (graph_->embeds() || !accepts(n, 0)) {
             return false;
         }
         return execute_all(n, 1, 0);
@@ -143,17 +178,65 @@ public:
     // GPU extension: `images` independent images of `rows` rows each in one
     // run (rows * images <= max_batch); self-attention stays within an image.
     // The reference encodes one image per run_rows call (S/models/clip.hpp:410).
+    // Graphs that embed, keep KV states or pixel-shuffle run one image per call.
     [[nodiscard]] bool run_images(std::size_t rows, std::size_t images) noexcept {
-        if (images == 0 || rows > graph_->max_batch() / std::max<std::size_t>(images, 1) || !accepts(rows * images, 0)) {
+        if (images == 0 || rows > graph_->max_batch() / std::max<std::size_t>(images, 1) || !accepts(rows * images, 0) ||
+            graph_->embeds() ||
+            (images > 1 && (!graph_->states().empty() || graph_->full_batch_only()))) {
             return false;
         }
         return execute_all(rows, images, 0);
     }
 
 private:
+    static constexpr std::uint64_t no_offset = ~std::uint64_t{0};
+
     bool accepts(std::size_t n, std::uint32_t pos) const noexcept {
         return arena_ != nullptr && n != 0 && n <= graph_->max_batch() &&
+               (!graph_->full_batch_only() || n == graph_->max_batch()) &&
                std::size_t{pos} + n <= graph_->position_limit();
+    }
+
+    // The matrices a node binds, in a fixed order (weight_offset_'s slots).
+    static std::array<const matrix_ref*, 2> bound_matrices(const node& n) noexcept {
+        return std::visit(
+            [](const auto& o) -> std::array<const matrix_ref*, 2> {
+                using T = std::decay_t<decltype(o)>;
+                if constexpr (std::is_same_v<T, op_matmul>) {
+                    return {&o.w, nullptr};
+                } else if constexpr (std::is_same_v<T, op_add_bias>) {
+                    return {&o.bias, nullptr};
+                } else if constexpr (std::is_same_v<T, op_rms_norm>) {
+                    return {&o.gamma, nullptr};
+                } else if constexpr (std::is_same_v<T, op_embed> || std::is_same_v<T, op_add_rows>) {
+                    return {&o.table, nullptr};
+                } else if constexpr (std::is_same_v<T, op_layer_norm>) {
+                    return {&o.gamma, &o.beta};
+                } else {
+                    return {nullptr, nullptr};
+                }
+            },
+            n);
+    }
+
+    // Rows of t a run of n rows (per image) uses.
+    std::size_t active_rows(tensor_id t, std::size_t n) const noexcept {
+        const tensor_desc& d = graph_->tensors()[t];
+        return d.batched ? n / d.row_div : 1;
+    }
+    std::size_t size_of(tensor_id t) const noexcept {
+        return graph_->tensors()[t].size;
+    }
+    int elementwise(std::uint32_t op, std::uint64_t a, std::uint64_t b, std::uint64_t out, std::uint64_t count,
+                    float scalar = 0.0f) noexcept {
+        syn_elementwise_desc d{};
+        d.a_offset = a;
+        d.b_offset = b;
+        d.out_offset = out;
+        d.count = count;
+        d.op = op;
+        d.scalar = scalar;
+        return syn_hip_elementwise(arena_, &d);
     }
 
     bool usable(tensor_id t, std::size_t floats) const noexcept {
@@ -178,6 +261,142 @@ private:
             }
         }
         return true;
+    }
+
+    int execute(const op_matmul& o, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        const std::size_t n = active_rows(o.in, rows * images);
+        if (type_of(o.w) == SYN_TYPE_F32) {
+            syn_matmul_desc d{};
+            d.w_offset = weight_offset_[i][0];
+            d.x_offset = plan_.offset[o.in];
+            d.bias_offset = no_offset;
+            d.out_offset = plan_.offset[o.out];
+            d.n = static_cast<std::uint32_t>(n);
+            d.rows = static_cast<std::uint32_t>(graph::rows(o.w));
+            d.cols = static_cast<std::uint32_t>(cols(o.w));
+            return syn_hip_matmul(arena_, &d);
+        }
+        syn_matmul_q_desc d{};
+        d.w_offset = weight_offset_[i][0];
+        d.x_offset = plan_.offset[o.in];
+        d.act_offset = plan_.offset[o.scratch];
+        d.bias_offset = no_offset;
+        d.out_offset = plan_.offset[o.out];
+        d.w_type = type_of(o.w);
+        d.n = static_cast<std::uint32_t>(n);
+        d.rows = static_cast<std::uint32_t>(graph::rows(o.w));
+        d.cols = static_cast<std::uint32_t>(cols(o.w));
+        return syn_hip_matmul_q(arena_, &d);
+    }
+    int execute(const op_add& o, std::size_t, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        return elementwise(SYN_ADD, plan_.offset[o.a], plan_.offset[o.b], plan_.offset[o.out],
+                           std::uint64_t{active_rows(o.a, rows * images)} * size_of(o.a));
+    }
+    int execute(const op_mul& o, std::size_t, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        return elementwise(SYN_MUL, plan_.offset[o.a], plan_.offset[o.b], plan_.offset[o.out],
+                           std::uint64_t{active_rows(o.a, rows * images)} * size_of(o.a));
+    }
+    int execute(const op_add_bias& o, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        const std::uint64_t row = size_of(o.in) * sizeof(float);
+        for (std::size_t r = 0; r < active_rows(o.in, rows * images); ++r) {
+            if (const int e = elementwise(SYN_ADD, plan_.offset[o.in] + r * row, weight_offset_[i][0],
+                                          plan_.offset[o.out] + r * row, size_of(o.in))) {
+                return e;
+            }
+        }
+        return SYN_HIP_OK;
+    }
+    int execute(const op_silu& o, std::size_t, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        return elementwise(SYN_SILU, plan_.offset[o.in], no_offset, plan_.offset[o.out],
+                           std::uint64_t{active_rows(o.in, rows * images)} * size_of(o.in));
+    }
+    int execute(const op_gelu& o, std::size_t, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        return elementwise(SYN_GELU, plan_.offset[o.in], no_offset, plan_.offset[o.out],
+                           std::uint64_t{active_rows(o.in, rows * images)} * size_of(o.in));
+    }
+    int execute(const op_softmax& o, std::size_t, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        syn_softmax_desc d{};
+        d.in_offset = plan_.offset[o.in];
+        d.out_offset = plan_.offset[o.out];
+        d.n = static_cast<std::uint32_t>(active_rows(o.in, rows * images));
+        d.size = static_cast<std::uint32_t>(size_of(o.in));
+        return syn_hip_softmax(arena_, &d);
+    }
+    int execute(const op_rms_norm& o, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        syn_norm_desc d{};
+        d.in_offset = plan_.offset[o.in];
+        d.weight_offset = weight_offset_[i][0];
+        d.out_offset = plan_.offset[o.out];
+        d.n = static_cast<std::uint32_t>(active_rows(o.in, rows * images));
+        d.size = static_cast<std::uint32_t>(size_of(o.in));
+        d.eps = o.eps;
+        return syn_hip_rms_norm(arena_, &d);
+    }
+    int execute(const op_layer_norm& o, std::size_t i, std::size_t rows, std::size_t images,
+                std::uint32_t) noexcept {
+        syn_layer_norm_desc d{};
+        d.in_offset = plan_.offset[o.in];
+        d.weight_offset = weight_offset_[i][0];
+        d.bias_offset = weight_offset_[i][1];
+        d.out_offset = plan_.offset[o.out];
+        d.n = static_cast<std::uint32_t>(active_rows(o.in, rows * images));
+        d.size = static_cast<std::uint32_t>(size_of(o.in));
+        d.eps = o.eps;
+        return syn_hip_layer_norm(arena_, &d);
+    }
+    int execute(const op_embed& o, std::size_t i, std::size_t rows, std::size_t, std::uint32_t) noexcept {
+        syn_embed_desc d{};
+        d.table_offset = weight_offset_[i][0];
+        d.out_offset = plan_.offset[o.out];
+        d.n_table_rows = static_cast<std::uint32_t>(graph::rows(o.table));
+        d.size = static_cast<std::uint32_t>(cols(o.table));
+        d.table_type = type_of(o.table);
+        return syn_hip_embed(arena_, &d, tokens_, static_cast<std::uint32_t>(rows));
+    }
+    // Each row times its position's temperature: a float quotient, the log
+    // in double, rounded to float (kernels::attn_temperature,
+    // S/kernels/elementwise.hpp:66-71).
+    int execute(const op_attn_temperature& o, std::size_t, std::size_t rows, std::size_t images,
+                std::uint32_t pos) noexcept {
+        const std::uint64_t row = size_of(o.in) * sizeof(float);
+        for (std::size_t img = 0; img < images; ++img) {
+            for (std::size_t r = 0; r < rows; ++r) {
+                const float q = std::floor(static_cast<float>(pos + r) / static_cast<float>(o.floor_len));
+                const auto t = static_cast<float>(std::log(static_cast<double>(q) + 1.0) * o.scale + 1.0);
+                const std::uint64_t at = (img * rows + r) * row;
+                if (const int e = elementwise(SYN_SCALE, plan_.offset[o.in] + at, no_offset, plan_.offset[o.out] + at,
+                                              size_of(o.in), t)) {
+                    return e;
+                }
+            }
+        }
+        return SYN_HIP_OK;
+    }
+    int execute(const op_last_row& o, std::size_t, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        const std::uint64_t row = size_of(o.in) * sizeof(float);
+        return syn_hip_copy(arena_, plan_.offset[o.out], plan_.offset[o.in] + (rows * images - 1) * row, row);
+    }
+    // Table row i added to row i of each image (rows start again per image).
+    int execute(const op_add_rows& o, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
+        const std::uint64_t image = std::uint64_t{rows} * size_of(o.in);
+        for (std::size_t img = 0; img < images; ++img) {
+            if (const int e = elementwise(SYN_ADD, plan_.offset[o.in] + img * image * sizeof(float),
+                                          weight_offset_[i][0], plan_.offset[o.out] + img * image * sizeof(float),
+                                          image)) {
+                return e;
+            }
+        }
+        return SYN_HIP_OK;
+    }
+    int execute(const op_pixel_shuffle& o, std::size_t, std::size_t rows, std::size_t, std::uint32_t) noexcept {
+        syn_pixel_shuffle_desc d{};
+        d.in_offset = plan_.offset[o.in];
+        d.out_offset = plan_.offset[o.out];
+        d.n = static_cast<std::uint32_t>(size_of(o.in));
+        d.grid_w = static_cast<std::uint32_t>(o.grid_w);
+        d.grid_h = static_cast<std::uint32_t>(rows / o.grid_w);
+        d.scale = static_cast<std::uint32_t>(o.scale);
+        return syn_hip_pixel_shuffle(arena_, &d);
     }
 
     int execute(const op_rope& r, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t pos) noexcept {
@@ -242,7 +461,9 @@ private:
 
     const compute_graph* graph_;
     memory_plan plan_;
-    std::vector<std::uint64_t> const_offset_;  // per node: its RoPE table, or ~0
+    std::vector<std::uint64_t> const_offset_;                  // per node: its RoPE table, or ~0
+    std::vector<std::array<std::uint64_t, 2>> weight_offset_;  // per node: its bound matrices
+    const std::uint32_t* tokens_ = nullptr;                    // the running batch's tokens
     std::vector<syn_kv_desc> kv_;
     std::size_t state_bytes_ = 0;
     syn_arena* arena_ = nullptr;

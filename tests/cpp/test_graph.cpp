@@ -21,8 +21,7 @@ graph_errc error_of(graph_builder&& b) {
 void llama_attention_wiring() {
     graph_builder b(4);
     const tensor_id q = b.input(32 * 128), k = b.input(8 * 128), v = b.input(8 * 128);
-    const float ts = std::pow(500000.0f, -2.0f / 128.0f);
-    const tensor_id qr = b.rope(q, 128, ts), kr = b.rope(k, 128, ts);
+    const tensor_id qr = b.rope(q, 128, 500000.0f), kr = b.rope(k, 128, 500000.0f);
     const state_id c = b.kv_cache(4097, 8, 128);
     const tensor_id out = b.attention(qr, kr, v, c, 32, 1.0f / std::sqrt(128.0f));
     b.output(out);

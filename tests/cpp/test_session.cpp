@@ -57,9 +57,8 @@ struct attention_layer {
 attention_layer build(const layer_case& c) {
     graph_builder b(c.max_batch);
     const tensor_id q = b.input(c.n_heads * c.hd), k = b.input(c.n_kv * c.hd), v = b.input(c.n_kv * c.hd);
-    const float ts = orc_rope_theta_scale(c.base, c.hd);
     const state_id cache = b.kv_cache(c.max_ctx, c.n_kv, c.hd);
-    const tensor_id out = b.attention(b.rope(q, c.hd, ts), b.rope(k, c.hd, ts), v, cache, c.n_heads,
+    const tensor_id out = b.attention(b.rope(q, c.hd, c.base), b.rope(k, c.hd, c.base), v, cache, c.n_heads,
                                       1.0f / std::sqrt(static_cast<float>(c.hd)));
     b.output(out);
     auto r = std::move(b).finalize();

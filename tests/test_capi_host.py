@@ -50,7 +50,8 @@ def test_descriptor_layouts_match_the_header(tmp_path):
                "syn_self_desc": capi.SelfDesc, "syn_rope_desc": capi.RopeDesc, "syn_embed_desc": capi.EmbedDesc,
                "syn_norm_desc": capi.NormDesc, "syn_matmul_desc": capi.MatmulDesc,
                "syn_elementwise_desc": capi.ElementwiseDesc, "syn_layer_norm_desc": capi.LayerNormDesc,
-               "syn_pixel_shuffle_desc": capi.PixelShuffleDesc, "syn_matmul_q_desc": capi.MatmulQDesc}
+               "syn_pixel_shuffle_desc": capi.PixelShuffleDesc, "syn_matmul_q_desc": capi.MatmulQDesc,
+               "syn_softmax_desc": capi.SoftmaxDesc}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, ct in structs.items():
         lines.append(f'printf("{cname} @sizeof %zu\\n", sizeof({cname}));')

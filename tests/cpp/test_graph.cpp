@@ -185,9 +185,120 @@ void planner_reuses_dead_tensors() {
     CHECK(p.naive_bytes == 11 * align_up(4096 * 4 * 4));
 }
 
+// The builder checks of the model ops (S/graph/graph.hpp:536-896): each
+// misuse fails with the reference's code at the node being added.
+void model_op_errors() {
+    static const float w64x16[64 * 16] = {}, v16[16] = {}, table[8 * 16] = {};
+    static const unsigned char q8[4 * 34] = {};
+    const matrix_ref w{weight_view{SYN_TYPE_F32, 64, 16, w64x16}};
+    const matrix_ref g16{weight_view{SYN_TYPE_F32, 1, 16, v16}};
+    const matrix_ref rows8{weight_view{SYN_TYPE_F32, 8, 16, table}};
+    const matrix_ref q8_row{weight_view{SYN_TYPE_Q8_0, 1, 128, q8}};
+    const auto err = [](auto&& build) {
+        graph_builder b(4);
+        const tensor_id x = b.input(16);
+        build(b, x);
+        return error_of(std::move(b));
+    };
+    const auto ok = [&](auto&& build) {
+        graph_builder b(4);
+        const tensor_id x = b.input(16);
+        b.output(build(b, x));
+        return error_of(std::move(b)) == graph_errc{};
+    };
+    CHECK(ok([&](graph_builder& b, tensor_id x) { return b.matmul(w, x); }));
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.matmul(w, b.matmul(w, x))); }) ==
+          graph_errc::size_mismatch);  // 64 values into a 16-column matrix
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.matmul(matrix_ref{}, x)); }) ==
+          graph_errc::size_mismatch);  // the empty matrix
+    CHECK(err([&](graph_builder& b, tensor_id x) {
+              b.output(b.matmul(matrix_ref{weight_view{SYN_TYPE_F32, 64, 16, nullptr}}, x));
+          }) == graph_errc::bad_parameter);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.add(x, b.matmul(w, x))); }) ==
+          graph_errc::size_mismatch);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.mul(x, b.last_row(x))); }) ==
+          graph_errc::size_mismatch);  // batched against one row (I8)
+    CHECK(ok([&](graph_builder& b, tensor_id x) { return b.add_bias(x, g16); }));
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.add_bias(x, rows8)); }) == graph_errc::size_mismatch);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.add_bias(b.matmul(w, x), q8_row)); }) ==
+          graph_errc::size_mismatch);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.rms_norm(x, w, 1e-5f)); }) ==
+          graph_errc::size_mismatch);
+    CHECK(ok([&](graph_builder& b, tensor_id x) { return b.softmax(b.silu(b.gelu(b.rms_norm(x, g16, 1e-5f)))); }));
+    CHECK(err([&](graph_builder& b, tensor_id) { b.output(b.embed(matrix_ref{})); }) == graph_errc::empty_tensor);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.attn_temperature(x, 0.5f, 0)); }) ==
+          graph_errc::bad_parameter);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.attn_temperature(x, NAN, 4)); }) ==
+          graph_errc::bad_parameter);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.attn_temperature(b.last_row(x), 0.5f, 4)); }) ==
+          graph_errc::bad_shape);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.last_row(b.last_row(x))); }) == graph_errc::bad_shape);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.layer_norm(x, g16, matrix_ref{}, -1.0f)); }) ==
+          graph_errc::bad_parameter);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.layer_norm(x, g16, rows8, 1e-5f)); }) ==
+          graph_errc::size_mismatch);
+    CHECK(ok([&](graph_builder& b, tensor_id x) { return b.layer_norm(x, g16, g16, 0.0f); }));
+    CHECK(ok([&](graph_builder& b, tensor_id x) { return b.add_rows(x, rows8); }));
+    CHECK(err([&](graph_builder& b, tensor_id x) {
+              b.output(b.add_rows(x, matrix_ref{weight_view{SYN_TYPE_F32, 3, 16, table}}));
+          }) == graph_errc::size_mismatch);  // fewer rows than max_batch
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.pixel_shuffle(x, 3, 2)); }) == graph_errc::bad_shape);
+    CHECK(err([&](graph_builder& b, tensor_id x) { b.output(b.pixel_shuffle(x, 2, 1)); }) == graph_errc::bad_shape);
+    CHECK(err([&](graph_builder& b, tensor_id x) {
+              b.output(b.pixel_shuffle(b.pixel_shuffle(x, 2, 2), 1, 2));
+          }) == graph_errc::bad_shape);  // its result is not per-token (I8)
+    CHECK(err([&](graph_builder& b, tensor_id x) {
+              const tensor_id y = b.silu(x);
+              b.output(y);
+              b.output(y);
+          }) == graph_errc::bad_output);
+    {
+        // a 2 x 2 grid of 4 patches merged into one row of 4 * 16; the graph
+        // then takes full batches only (I9)
+        graph_builder b(4);
+        const tensor_id x = b.input(16);
+        const tensor_id y = b.pixel_shuffle(x, 2, 2);
+        b.output(b.matmul(matrix_ref{weight_view{SYN_TYPE_F32, 8, 64, w64x16}}, y));
+        auto r = std::move(b).finalize();
+        CHECK(r.has_value());
+        if (r) {
+            const compute_graph& g = r.value();
+            CHECK(g.full_batch_only() && !g.embeds());
+            CHECK(g.rows(y) == 1 && g.tensors()[y].size == 64 && g.tensors()[y].row_div == 4);
+            CHECK(plan_is_valid(g, plan(g)));
+        }
+    }
+    {
+        // embed bounds the tokens a run accepts; matmul on quantized
+        // weights sizes its activation scratch through the library
+        graph_builder b(2);
+        const tensor_id x = b.embed(rows8);
+        const tensor_id y = b.matmul(matrix_ref{weight_view{SYN_TYPE_Q8_0, 4, 16 * 2, q8}}, b.add(x, x));
+        b.output(y);
+        auto r = std::move(b).finalize();
+        CHECK(!r.has_value() && r.error().code == graph_errc::size_mismatch);  // 16 values, 32 columns
+        graph_builder b2(2);
+        const tensor_id x2 = b2.embed(rows8);
+        const tensor_id h = b2.matmul(matrix_ref{weight_view{SYN_TYPE_F32, 2, 16, w64x16}}, x2);
+        const tensor_id y2 = b2.matmul(matrix_ref{weight_view{SYN_TYPE_Q8_0, 4, 32, q8}},
+                                       b2.matmul(matrix_ref{weight_view{SYN_TYPE_F32, 32, 2, w64x16}}, h));
+        b2.output(y2);
+        auto r2 = std::move(b2).finalize();
+        CHECK(r2.has_value());
+        if (r2) {
+            const compute_graph& g = r2.value();
+            CHECK(g.embeds() && g.token_limit() == 8 && !g.full_batch_only());
+            const auto& mm = std::get<op_matmul>(g.nodes().back());
+            CHECK(g.tensors()[mm.scratch].bytes == syn_hip_matmul_q_act_bytes(SYN_TYPE_Q8_0, 2, 32));
+            CHECK(plan_is_valid(g, plan(g)));
+        }
+    }
+}
+
 }  // namespace
 
 int main() {
+    model_op_errors();
     llama_attention_wiring();
     kv_cache_errors();
     attention_errors();

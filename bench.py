@@ -42,7 +42,7 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
 # HBM bytes one config-2 decode step moves (split + merge kernels), from two
 # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a copy of known
 # size; profiles/decode_c2_pmc_traffic.md has the runs and the factors.
-DECODE_TRAFFIC_BYTES = 18_419_688
+DECODE_TRAFFIC_BYTES = 18_253_056
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 matrix, TFLOP/s
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 matrix, TOP/s
 

@@ -6,7 +6,11 @@
 // llama.cpp computed for the reference's tiny models
 // (tests/sdk/llama_golden.cpp:58-83).
 //
-// Usage: test_model_session <dump dir> <max|rms> <bound>. The directory
+// The same program checks the image encoder's graph (layer_norm, gelu,
+// add_rows, self_attention, pixel_shuffle) against clip_tiny's golden
+// embeddings when the dump's config says "model clip".
+//
+// Usage: test_model_session <dump dir> <max|rms|rowrms> <bound>. The directory
 // holds what tests/test_host_cpp.py extracts from a fixture: config.txt
 // (key value), manifest.txt (name type rows cols offset bytes) over
 // weights.bin, tokens.txt and logits.bin (tokens x n_vocab f32). Each token
@@ -159,6 +163,82 @@ bool close(const float* got, const float* ref, std::size_t n, const std::string&
     return std::isfinite(*err) && *err < bound && same_argmax;
 }
 
+// The image encoder, as S/models/clip.hpp:300-380 builds it: patch
+// projection with add_bias and add_rows (position embeddings), per layer
+// layer_norm, q/k/v, self_attention, the output projection and the GELU
+// MLP with residual adds, then post layer_norm (when the file has it),
+// pixel_shuffle and the projector matmul.
+struct clip_graph {
+    compute_graph g;
+    tensor_id patches, embeddings;
+};
+
+clip_graph build_clip(const model_dump& m) {
+    const std::size_t P = m.count("n_patches"), E = m.count("n_embd"), H = m.count("n_head");
+    graph_builder b(P);
+    const float eps = m.f32("eps");
+    const auto linear = [&](const std::string& w, const std::string& bias, tensor_id x) {
+        const tensor_id y = b.matmul(m.w(w), x);
+        return m.has(bias) ? b.add_bias(y, m.w(bias)) : y;
+    };
+    const tensor_id patches = b.input(m.count("patch_floats"));
+    tensor_id x = b.add_rows(linear("patch.w", "patch.b", patches), m.w("pos"));
+    for (std::size_t l = 0; l < m.count("n_layer"); ++l) {
+        const std::string p = "v.blk." + std::to_string(l) + ".";
+        const tensor_id h = b.layer_norm(x, m.w(p + "ln1.weight"), m.w(p + "ln1.bias"), eps);
+        const tensor_id a = b.self_attention(linear(p + "attn_q.weight", p + "attn_q.bias", h),
+                                             linear(p + "attn_k.weight", p + "attn_k.bias", h),
+                                             linear(p + "attn_v.weight", p + "attn_v.bias", h), H,
+                                             1.0f / std::sqrt(static_cast<float>(E / H)));
+        x = b.add(linear(p + "attn_out.weight", p + "attn_out.bias", a), x);
+        const tensor_id h2 = b.layer_norm(x, m.w(p + "ln2.weight"), m.w(p + "ln2.bias"), eps);
+        x = b.add(x, linear(p + "down.w", p + "down.b", b.gelu(linear(p + "up.w", p + "up.b", h2))));
+    }
+    if (m.has("post.w")) {
+        x = b.layer_norm(x, m.w("post.w"), m.w("post.b"), eps);
+    }
+    const tensor_id emb = b.matmul(m.w("fc"), b.pixel_shuffle(x, m.count("grid"), m.count("scale_factor")));
+    b.output(emb);
+    auto r = std::move(b).finalize();
+    CHECK(r.has_value());
+    if (!r.has_value()) {
+        std::fprintf(stderr, "graph error %s at node %zu\n", std::string(to_string(r.error().code)).c_str(),
+                     r.error().node);
+        std::exit(1);
+    }
+    return {std::move(r).value(), patches, emb};
+}
+
+// Per output row, rms(got - ref) / rms(ref) (tests/sdk/clip_golden.cpp:22-35).
+int run_clip(const model_dump& m, const std::string& dir, double bound) {
+    const clip_graph cg = build_clip(m);
+    session s(cg.g);
+    CHECK(s.status() == SYN_HIP_OK);
+    const std::vector<char> raw = slurp(dir + "/patches.bin");
+    std::vector<float> patches(raw.size() / sizeof(float));
+    std::copy(raw.begin(), raw.end(), reinterpret_cast<char*>(patches.data()));
+    const std::size_t rows = m.count("n_tokens"), width = m.count("n_embd_text");
+    std::vector<float> got(rows * width);
+    CHECK(s.write(cg.patches, patches));
+    CHECK(s.run_rows(m.count("n_patches")));
+    CHECK(!s.run_rows(m.count("n_patches") - 1));  // a pixel-shuffle graph takes full batches only
+    CHECK(s.read(cg.embeddings, got));
+    CHECK(m.logits.size() == got.size());
+    double worst = 0;
+    for (std::size_t r = 0; r < rows; ++r) {
+        double d2 = 0, r2 = 0;
+        for (std::size_t i = 0; i < width; ++i) {
+            const double d = static_cast<double>(got[r * width + i]) - m.logits[r * width + i];
+            d2 += d * d;
+            r2 += static_cast<double>(m.logits[r * width + i]) * m.logits[r * width + i];
+        }
+        worst = std::max(worst, std::sqrt(d2 / r2));
+    }
+    std::printf("%s, image encoder: worst per-token rel rms %.3g (bound %g)\n", dir.c_str(), worst, bound);
+    CHECK(std::isfinite(worst) && worst < bound);
+    CHECK_DONE();
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -169,6 +249,9 @@ int main(int argc, char** argv) {
     const model_dump m = load(argv[1]);
     const std::string metric = argv[2];
     const double bound = std::strtod(argv[3], nullptr);
+    if (m.cfg.count("model") != 0 && m.cfg.at("model") == "clip") {
+        return run_clip(m, argv[1], bound);
+    }
     const std::size_t n_vocab = m.count("n_vocab"), n_tok = m.tokens.size();
     CHECK(n_tok > 0 && m.logits.size() == n_tok * n_vocab);
 

@@ -95,3 +95,57 @@ def test_model_graph_through_the_session(tmp_path, name):
     against llama.cpp's logits for the reference's tiny models."""
     _dump_model(name, tmp_path)
     _run("test_model_session", str(tmp_path), *MODEL_BOUNDS[name])
+
+
+def _dump_clip(out: pathlib.Path) -> None:
+    """clip_tiny's weights under the names test_model_session reads, its
+    unfolded image and golden embeddings (the projector file's up/down pair
+    taken in whichever order it is stored, S/models/clip.hpp:318-323)."""
+    import numpy as np
+
+    from synapse_amd.clip import read_config, unfold_patches
+    from synapse_amd.gguf import GGUFFile
+
+    model = GGUFFile(DATA / "clip_tiny.gguf")
+    golden = GGUFFile(DATA / "clip_tiny_golden.gguf")
+    c = read_config(model)
+    E, F = c.n_embd, c.n_ff
+    names = {"patch.w": "v.patch_embd.weight", "patch.b": "v.patch_embd.bias", "pos": "v.position_embd.weight",
+             "post.w": "v.post_ln.weight", "post.b": "v.post_ln.bias", "fc": "mm.model.fc.weight"}
+    for l in range(c.n_layer):
+        b = f"v.blk.{l}."
+        for s in ("ln1.weight", "ln1.bias", "attn_q.weight", "attn_q.bias", "attn_k.weight", "attn_k.bias",
+                  "attn_v.weight", "attn_v.bias", "attn_out.weight", "attn_out.bias", "ln2.weight", "ln2.bias"):
+            names[b + s] = b + s
+        up, down = ("ffn_down", "ffn_up") if model.tensors[b + "ffn_down.weight"].shape[0] == E else ("ffn_up",
+                                                                                                      "ffn_down")
+        names.update({b + "up.w": b + up + ".weight", b + "up.b": b + up + ".bias", b + "down.w": b + down + ".weight",
+                      b + "down.b": b + down + ".bias"})
+    blob, lines = bytearray(), []
+    for key, tname in names.items():
+        if tname not in model.tensors:
+            continue
+        a = np.ascontiguousarray(model.tensor(tname), dtype=np.float32)
+        a = a.reshape(1, -1) if a.ndim == 1 else a.reshape(a.shape[0], -1)  # the patch kernel: (channel, y, x)
+        rows, cols = a.shape
+        raw = a.tobytes()
+        lines.append(f"{key} 0 {rows} {cols} {len(blob)} {len(raw)}")
+        blob += raw + bytes(-len(raw) % 64)
+    (out / "weights.bin").write_bytes(bytes(blob))
+    (out / "manifest.txt").write_text("\n".join(lines) + "\n")
+    cfg = {"model": "clip", "n_layer": c.n_layer, "n_embd": E, "n_head": c.n_head, "n_ff": F,
+           "eps": repr(float(np.float32(c.eps))), "patch_floats": c.patch_floats, "n_patches": c.n_patches,
+           "grid": c.grid, "scale_factor": c.scale_factor, "n_tokens": c.n_tokens, "n_embd_text": c.n_embd_text}
+    (out / "config.txt").write_text("".join(f"{k} {v}\n" for k, v in cfg.items()))
+    image = np.asarray(golden.tensor("image"), np.float32)
+    (out / "patches.bin").write_bytes(np.ascontiguousarray(unfold_patches(c, image), np.float32).tobytes())
+    (out / "logits.bin").write_bytes(np.ascontiguousarray(golden.tensor("embeddings"), np.float32).tobytes())
+
+
+@pytest.mark.gpu
+def test_image_encoder_graph_through_the_session(tmp_path):
+    """layer_norm, gelu, add_rows, self_attention and pixel_shuffle through
+    graph_builder and session against clip_tiny's golden embeddings, at the
+    device bound of tests/test_clip_golden.py (per-token rel rms < 1e-3)."""
+    _dump_clip(tmp_path)
+    _run("test_model_session", str(tmp_path), "rowrms", "1e-3")

@@ -281,8 +281,10 @@ int syn_hip_matmul_q(syn_arena* arena, const syn_matmul_q_desc* desc);
  * (op_mul), SYN_SILU_MUL silu(a) * b (op_silu then op_mul), SYN_SCALE
  * a * scalar (kernels::scale, as op_attn_temperature applies it), SYN_GELU
  * gelu(a) in ggml's binary16-rounded form (op_gelu), SYN_SILU
- * a / (1 + exp(-a)) (op_silu). out may alias a or b. */
-enum { SYN_ADD = 0, SYN_MUL = 1, SYN_SILU_MUL = 2, SYN_SCALE = 3, SYN_GELU = 4, SYN_SILU = 5 };
+ * a / (1 + exp(-a)) (op_silu), SYN_ADD_BIAS a + b[e % period], the
+ * period floats of b added to every row (op_add_bias,
+ * S/graph/session.hpp:306-312). out may alias a or b. */
+enum { SYN_ADD = 0, SYN_MUL = 1, SYN_SILU_MUL = 2, SYN_SCALE = 3, SYN_GELU = 4, SYN_SILU = 5, SYN_ADD_BIAS = 6 };
 
 typedef struct syn_elementwise_desc {
     uint64_t a_offset;
@@ -291,6 +293,8 @@ typedef struct syn_elementwise_desc {
     uint64_t count;
     uint32_t op;
     float scalar;
+    uint32_t period;     /* SYN_ADD_BIAS: floats of b, dividing count */
+    uint32_t reserved;
 } syn_elementwise_desc;
 
 int syn_hip_elementwise(syn_arena* arena, const syn_elementwise_desc* desc);

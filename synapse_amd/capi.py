@@ -69,7 +69,7 @@ class MatmulDesc(ctypes.Structure):
 
 class ElementwiseDesc(ctypes.Structure):
     _fields_ = [("a_offset", u64), ("b_offset", u64), ("out_offset", u64), ("count", u64), ("op", u32),
-                ("scalar", f32)]
+                ("scalar", f32), ("period", u32), ("reserved", u32)]
 
 
 class LayerNormDesc(ctypes.Structure):
@@ -86,7 +86,7 @@ class SoftmaxDesc(ctypes.Structure):
     _fields_ = [("in_offset", u64), ("out_offset", u64), ("n", u32), ("size", u32)]
 
 
-SYN_ADD, SYN_MUL, SYN_SILU_MUL, SYN_SCALE, SYN_GELU, SYN_SILU = 0, 1, 2, 3, 4, 5
+SYN_ADD, SYN_MUL, SYN_SILU_MUL, SYN_SCALE, SYN_GELU, SYN_SILU, SYN_ADD_BIAS = 0, 1, 2, 3, 4, 5, 6
 
 
 # name -> (restype, argtypes); every symbol include/synapse_hip.h declares.

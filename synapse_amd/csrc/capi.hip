@@ -920,7 +920,7 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
     if (d == nullptr) {
         return fail(SYN_HIP_EINVAL, "null descriptor");
     }
-    if (d->op > SYN_SILU) {
+    if (d->op > SYN_ADD_BIAS) {
         return fail(SYN_HIP_EINVAL, "elementwise: op %u", d->op);
     }
     if (d->count == 0) {
@@ -937,7 +937,16 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
         return e;
     }
     const float* b = nullptr;
-    if (d->op != SYN_SCALE && d->op != SYN_GELU && d->op != SYN_SILU) {
+    if (d->op == SYN_ADD_BIAS) {
+        if (d->period == 0 || d->count % d->period != 0) {
+            return fail(SYN_HIP_EINVAL, "elementwise: period %u for count %llu", d->period,
+                        static_cast<unsigned long long>(d->count));
+        }
+        if (int e = check_range(a, d->b_offset, uint64_t{d->period} * 4, 4, "elementwise bias")) {
+            return e;
+        }
+        b = reinterpret_cast<const float*>(a->base + d->b_offset);
+    } else if (d->op != SYN_SCALE && d->op != SYN_GELU && d->op != SYN_SILU) {
         if (int e = check_range(a, d->b_offset, bytes, 4, "elementwise b")) {
             return e;
         }
@@ -945,7 +954,7 @@ int syn_hip_elementwise(syn_arena* a, const syn_elementwise_desc* d) {
     }
     return hip_status(syn::launch_elementwise(reinterpret_cast<const float*>(a->base + d->a_offset), b,
                                               reinterpret_cast<float*>(a->base + d->out_offset), d->count, d->op,
-                                              d->scalar, a->stream),
+                                              d->scalar, d->period, a->stream),
                       "elementwise launch");
 }
 

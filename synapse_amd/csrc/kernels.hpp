@@ -133,6 +133,7 @@ enum elementwise_op : uint32_t {
     elementwise_scale = 3,     // a * scalar
     elementwise_gelu = 4,      // gelu(a), ggml's binary16-rounded tanh form
     elementwise_silu = 5,      // silu(a)
+    elementwise_add_bias = 6,  // a + b[e % period]
 };
 hipError_t launch_embed(const float* table, float* out, const embed_tokens& t, uint32_t n, uint32_t size,
                         hipStream_t stream);
@@ -142,6 +143,7 @@ hipError_t launch_rms_norm(const float* in, const float* gamma, float* out, uint
 hipError_t launch_matmul(const float* w, const float* x, const float* bias, float* out, uint32_t n, uint32_t rows,
                          uint32_t cols, hipStream_t stream);
 hipError_t launch_elementwise(const float* a, const float* b, float* out, uint64_t count, uint32_t op, float scalar,
+                              uint32_t period,
                               hipStream_t stream);
 // Quantized weights (quant.hip), ggml type numbers.
 constexpr uint32_t qtype_q4_0 = 2, qtype_q5_0 = 6, qtype_q8_0 = 8, qtype_q4_k = 12, qtype_q6_k = 14;

@@ -100,7 +100,7 @@ __device__ __forceinline__ float gelu_f16_table(float x) {
 
 // Element-wise ops (S/kernels/elementwise.hpp:28-81).
 __global__ __launch_bounds__(256) void elementwise_kernel(const float* a, const float* b, float* out, uint64_t count,
-                                                          uint32_t op, float scalar) {
+                                                          uint32_t op, float scalar, uint32_t period) {
     for (uint64_t e = blockIdx.x * 256ull + threadIdx.x; e < count; e += gridDim.x * 256ull) {
         const float x = a[e];
         float y;
@@ -121,6 +121,9 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const float* a, const 
             break;
         case elementwise_silu:  // kernels::silu
             y = x / (1.0f + expf(-x));
+            break;
+        case elementwise_add_bias:  // kernels::add_bias on every row
+            y = x + b[e % period];
             break;
         default:  // elementwise_scale
             y = x * scalar;
@@ -283,8 +286,8 @@ hipError_t launch_pixel_shuffle(const float* in, float* out, uint32_t n, uint32_
 }
 
 hipError_t launch_elementwise(const float* a, const float* b, float* out, uint64_t count, uint32_t op, float scalar,
-                              hipStream_t stream) {
-    elementwise_kernel<<<grid_for(count), 256, 0, stream>>>(a, b, out, count, op, scalar);
+                              uint32_t period, hipStream_t stream) {
+    elementwise_kernel<<<grid_for(count), 256, 0, stream>>>(a, b, out, count, op, scalar, period);
     return hipGetLastError();
 }
 

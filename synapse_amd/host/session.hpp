@@ -228,7 +228,7 @@ private:
         return graph_->tensors()[t].size;
     }
     int elementwise(std::uint32_t op, std::uint64_t a, std::uint64_t b, std::uint64_t out, std::uint64_t count,
-                    float scalar = 0.0f) noexcept {
+                    float scalar = 0.0f, std::uint32_t period = 0) noexcept {
         syn_elementwise_desc d{};
         d.a_offset = a;
         d.b_offset = b;
@@ -236,6 +236,7 @@ private:
         d.count = count;
         d.op = op;
         d.scalar = scalar;
+        d.period = period;
         return syn_hip_elementwise(arena_, &d);
     }
 
@@ -297,14 +298,9 @@ private:
                            std::uint64_t{active_rows(o.a, rows * images)} * size_of(o.a));
     }
     int execute(const op_add_bias& o, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
-        const std::uint64_t row = size_of(o.in) * sizeof(float);
-        for (std::size_t r = 0; r < active_rows(o.in, rows * images); ++r) {
-            if (const int e = elementwise(SYN_ADD, plan_.offset[o.in] + r * row, weight_offset_[i][0],
-                                          plan_.offset[o.out] + r * row, size_of(o.in))) {
-                return e;
-            }
-        }
-        return SYN_HIP_OK;
+        return elementwise(SYN_ADD_BIAS, plan_.offset[o.in], weight_offset_[i][0], plan_.offset[o.out],
+                           std::uint64_t{active_rows(o.in, rows * images)} * size_of(o.in), 0.0f,
+                           static_cast<std::uint32_t>(size_of(o.in)));
     }
     int execute(const op_silu& o, std::size_t, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
         return elementwise(SYN_SILU, plan_.offset[o.in], no_offset, plan_.offset[o.out],

@@ -1,6 +1,7 @@
-"""GPU checks of the two graph ops the C++ session added to the device:
-op_silu (SYN_SILU, kernels::silu) and op_softmax (syn_hip_softmax,
-kernels::softmax, S/kernels/elementwise.hpp:169-199). Both are pinned by
+"""GPU checks of the graph ops the C++ session added to the device:
+op_silu (SYN_SILU, kernels::silu), op_add_bias over every row in one launch
+(SYN_ADD_BIAS) and op_softmax (syn_hip_softmax, kernels::softmax,
+S/kernels/elementwise.hpp:169-199). Both are pinned by
 their closed forms, evaluated in float64 on the same inputs: silu within
 4 float ulps (expf, the sum and the quotient each round), softmax within
 1e-6 relative per element of exp over the float differences x - max, rows summing to 1,
@@ -69,3 +70,19 @@ def test_softmax_in_place_and_rejects_partial_overlap(arena):
     np.testing.assert_array_equal(got, _softmax(arena, x))
     bad = capi.SoftmaxDesc(off, off + 4 * 300, 3, 300)
     assert lib().syn_hip_softmax(arena.handle, ctypes.byref(bad)) != 0
+
+
+@pytest.mark.parametrize("rows,size", [(1, 64), (7, 100), (64, 4096), (3, 1)])
+def test_add_bias_broadcasts_every_row(arena, rows, size):
+    """SYN_ADD_BIAS (op_add_bias): the same float additions as a row loop,
+    bit for bit; a period that does not divide the count is refused."""
+    g = wl.rng(rows * size)
+    x = wl.normal(g, (rows, size)).astype(np.float32)
+    bias = wl.normal(g, (size,)).astype(np.float32)
+    a, b, out = arena.put(x), arena.put(bias), arena.alloc(x.nbytes)
+    d = capi.ElementwiseDesc(a, b, out, x.size, capi.SYN_ADD_BIAS, 0.0, size, 0)
+    check(lib().syn_hip_elementwise(arena.handle, ctypes.byref(d)))
+    np.testing.assert_array_equal(arena.download(out, x.shape, np.float32), x + bias[None, :])
+    if size > 1:
+        bad = capi.ElementwiseDesc(a, b, out, x.size, capi.SYN_ADD_BIAS, 0.0, size + 1, 0)
+        assert lib().syn_hip_elementwise(arena.handle, ctypes.byref(bad)) != 0

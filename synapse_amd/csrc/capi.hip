@@ -128,7 +128,9 @@ uint64_t decode_scratch_bytes(uint32_t splits, uint32_t n_kv, uint32_t group, ui
 // scratch, launches. kv_dtype types the sequences' k_new / v_new rows.
 int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n_kv, uint32_t hd, uint32_t group,
                float scale, uint32_t q_dtype, uint32_t kv_dtype, uint64_t scratch_offset, uint64_t scratch_bytes) {
-    syn::decode_args args{};
+    if (n == 0 || n > syn::decode_max_seqs) {
+        return fail(SYN_HIP_EINVAL, "decode: %u sequences in one launch", n);
+    }
     uint64_t positions = 0;
     uint32_t max_len = 0;
     for (uint32_t i = 0; i < n; ++i) {
@@ -141,29 +143,30 @@ int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n
             return fail(SYN_HIP_EUNSUPPORTED, "decode: a split or V^T row span exceeds 2^31 bytes");
         }
     }
+    syn::decode_params prm{};
     uint32_t splits = 0;
     uint32_t merge_blocks = 0;
+    syn::decode_seq table[syn::decode_max_seqs];
     for (uint32_t i = 0; i < n; ++i) {
-        args.seq[i] = seqs[i];
-        args.seq[i].block0 = splits;
-        args.seq[i].n_splits = (seqs[i].len + chunk - 1) / chunk;
-        args.seq[i].merge0 = merge_blocks;
-        args.block0s[i] = splits;
-        args.merge0s[i] = merge_blocks;
-        splits += args.seq[i].n_splits;
-        if (args.seq[i].n_splits > 1) {
+        table[i] = seqs[i];
+        table[i].block0 = splits;
+        table[i].n_splits = (seqs[i].len + chunk - 1) / chunk;
+        table[i].merge0 = merge_blocks;
+        splits += table[i].n_splits;
+        if (table[i].n_splits > 1) {
             merge_blocks += n_kv * group;
         }
     }
-    args.n_seqs = n;
-    args.n_kv = n_kv;
-    args.hd = hd;
-    args.group = group;
-    args.row = n_kv * hd;
-    args.chunk = chunk;
-    args.kv_dtype = kv_dtype;
-    args.merge_blocks = merge_blocks;
-    args.scale_log2e = scale * syn::log2e;
+    prm.n_kv = n_kv;
+    prm.hd = hd;
+    prm.group = group;
+    prm.row = n_kv * hd;
+    prm.chunk = chunk;
+    prm.kv_dtype = kv_dtype;
+    prm.total_slots = splits * n_kv;
+    prm.merge_blocks = merge_blocks;
+    prm.n_seqs = n;
+    prm.scale_log2e = scale * syn::log2e;
     if (merge_blocks > 0) {
         const uint64_t need = decode_scratch_bytes(splits, n_kv, group, hd);
         if (need > scratch_bytes) {
@@ -173,11 +176,20 @@ int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n
         if (int e = check_range(a, scratch_offset, need, 16, "decode scratch")) {
             return e;
         }
-        float* part = reinterpret_cast<float*>(a->base + scratch_offset);
-        args.part_o = part;
-        args.part_ml = part + uint64_t{splits} * n_kv * group * hd;
+        prm.part = reinterpret_cast<float*>(a->base + scratch_offset);
     }
-    return hip_status(syn::launch_decode(args, splits, q_dtype, a->stream), "decode launch");
+    if (n == 1) {
+        syn::decode_one_args one{prm, table[0]};
+        return hip_status(syn::launch_decode(one, q_dtype, a->stream), "decode launch");
+    }
+    syn::decode_batch_args batch{};
+    batch.p = prm;
+    for (uint32_t i = 0; i < n; ++i) {
+        batch.seq[i] = table[i];
+        batch.block0s[i] = table[i].block0;
+        batch.merge0s[i] = table[i].merge0;
+    }
+    return hip_status(syn::launch_decode(batch, q_dtype, a->stream), "decode launch");
 }
 
 int check_attn(const syn_arena* a, const syn_attn_desc* d, bool with_new_rows) {
@@ -248,6 +260,7 @@ bool decode_shape(const syn_attn_desc* d) {
     const syn_kv_desc& c = d->cache;
     const uint32_t len = d->pos + 1;
     return d->n == 1 && fast_shape(c.head_dim) && d->n_heads / c.n_kv_heads <= 16 &&
+
            syn::decode_fits(syn::decode_choose_chunk(len, c.n_kv_heads, len), c.n_kv_heads * c.head_dim, c.head_dim,
                             c.ctx_stride);
 }
@@ -517,9 +530,10 @@ uint64_t syn_hip_attend_batch_scratch_bytes(const syn_seq_desc* seqs, uint32_t n
     }
     const uint32_t n_kv = seqs[0].cache.n_kv_heads;
     const uint32_t hd = seqs[0].cache.head_dim;
+    const uint32_t per = syn::decode_max_seqs;
     uint64_t worst = 0;
-    for (uint32_t b0 = 0; b0 < n_seqs; b0 += syn::decode_max_seqs) {
-        const uint32_t nb = std::min(n_seqs - b0, syn::decode_max_seqs);
+    for (uint32_t b0 = 0; b0 < n_seqs; b0 += per) {
+        const uint32_t nb = std::min(n_seqs - b0, per);
         uint64_t positions = 0;
         uint32_t max_len = 0;
         for (uint32_t i = 0; i < nb; ++i) {
@@ -573,9 +587,10 @@ int syn_hip_attend_batch(syn_arena* a, const syn_seq_desc* seqs, uint32_t n_seqs
         return fail(SYN_HIP_EINVAL, "attend_batch: %u query heads on %u KV heads", n_heads, n_kv);
     }
     const uint32_t group = n_heads / n_kv;
+    const uint32_t per = syn::decode_max_seqs;
     bool fits = true;
-    for (uint32_t b0 = 0; b0 < n_seqs; b0 += syn::decode_max_seqs) {
-        const uint32_t nb = std::min(n_seqs - b0, syn::decode_max_seqs);
+    for (uint32_t b0 = 0; fits && b0 < n_seqs; b0 += per) {
+        const uint32_t nb = std::min(n_seqs - b0, per);
         uint64_t positions = 0;
         uint32_t max_len = 0;
         for (uint32_t i = 0; i < nb; ++i) {
@@ -606,8 +621,8 @@ int syn_hip_attend_batch(syn_arena* a, const syn_seq_desc* seqs, uint32_t n_seqs
         }
         return SYN_HIP_OK;
     }
-    for (uint32_t b0 = 0; b0 < n_seqs; b0 += syn::decode_max_seqs) {
-        const uint32_t nb = std::min(n_seqs - b0, syn::decode_max_seqs);
+    for (uint32_t b0 = 0; b0 < n_seqs; b0 += per) {
+        const uint32_t nb = std::min(n_seqs - b0, per);
         syn::decode_seq ds[syn::decode_max_seqs];
         for (uint32_t i = 0; i < nb; ++i) {
             const syn_seq_desc& s = seqs[b0 + i];

@@ -11,7 +11,9 @@
 //   S^T (16 positions x 16 heads) = K (16 x hd) . q^T       2 tiles, hd/32 MFMAs each
 //   O   (16 heads x 16 dims)     += P (16 x 32 positions) . V   hd/16 MFMAs
 // K rows and V^T rows are the MFMA operands exactly as they sit in memory
-// (one 16-byte load per lane and k-step), and the S^T tiles are laid out so
+// (one 16-byte load per lane and k-step; the score contraction visits the
+// dims in the order 32*st + 8*G, so one load instruction reads 64
+// contiguous bytes of each of its 16 rows), and the S^T tiles are laid out so
 // their accumulator registers ARE the P operand of the second product: the
 // position order inside a tile is permuted so that lane group G holds the 8
 // consecutive positions 8G..8G+7 of the block. No LDS, no shuffles on the
@@ -24,9 +26,11 @@
 // than one split then needs its splits combined: each block writes its
 // unnormalised partial (max, sum, O) to scratch, and a second small kernel on
 // the same stream merges them, one block per (sequence, query head). The
-// kernel boundary is what makes the partials visible: an in-kernel
-// "last block merges" handoff needs an agent-scope release per block, which
-// on this multi-XCD part writes back the whole L2 each time and costs far
+// kernel boundary is what makes the partials visible. Merging inside this
+// kernel was built and measured slower: the partials must be stored
+// write-through or read with agent-scope loads (plain loads on another CU
+// never see them), and the handoff -- store acknowledged, arrival counter,
+// poll, partial loads -- costs three or four loaded memory round trips,
 // more than the second launch. The merge stages through LDS: one wave turns
 // the splits' (max, sum) into weights with shuffles, then all threads stream
 // the partial outputs with independent 16-byte loads. Each output sums its
@@ -34,7 +38,7 @@
 //
 // A single-token step passes its new K, V row (k_new, v_new): the block whose
 // split ends at that position rounds it to binary16, attends it from
-// registers and stores it into the cache, so the step is one launch.
+// registers and stores it into the cache, so no separate append launch.
 
 #include "kernels.hpp"
 
@@ -60,20 +64,38 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // The sequence a block belongs to: starts[] is non-decreasing, and sequence
 // i owns blocks [starts[i], starts[i+1]). All loads are independent, so they
-// go out as one batch; a single-sequence launch needs none.
-template <bool MULTI>
+// go out as one batch.
 __device__ __forceinline__ uint32_t find_seq(const uint32_t* starts, uint32_t n, uint32_t x) {
-    if constexpr (!MULTI) {
-        return 0;
-    } else {
-        uint32_t si = 0;
+    uint32_t si = 0;
 #pragma unroll
-        for (uint32_t i = 1; i < decode_max_seqs; ++i) {
-            si += (i < n && x >= starts[i]) ? 1u : 0u;
-        }
-        return si;
+    for (uint32_t i = 1; i < decode_max_seqs; ++i) {
+        si += (i < n && x >= starts[i]) ? 1u : 0u;
     }
+    return si;
 }
+
+// One sequence per launch (a decode step) or a table of them (ragged batch):
+// the kernels see either through these.
+template <class A>
+struct decode_traits;
+template <>
+struct decode_traits<decode_one_args> {
+    static constexpr bool multi = false;
+    __device__ static const decode_seq& seq(const decode_one_args& a, uint32_t) { return a.s; }
+    __device__ static uint32_t find(const decode_one_args&, uint32_t) { return 0; }
+    __device__ static uint32_t find_merge(const decode_one_args&, uint32_t) { return 0; }
+};
+template <>
+struct decode_traits<decode_batch_args> {
+    static constexpr bool multi = true;
+    __device__ static const decode_seq& seq(const decode_batch_args& a, uint32_t i) { return a.seq[i]; }
+    __device__ static uint32_t find(const decode_batch_args& a, uint32_t sb) {
+        return find_seq(a.block0s, a.p.n_seqs, sb);
+    }
+    __device__ static uint32_t find_merge(const decode_batch_args& a, uint32_t u) {
+        return find_seq(a.merge0s, a.p.n_seqs, u);
+    }
+};
 
 // LDS of the split kernel: the group's q as given (f32 size, the larger),
 // the new K and V row of one head (likewise), per-wave (max, sum), then the
@@ -95,19 +117,21 @@ constexpr int vmcnt_imm(int n) {
     return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
-template <int HDP, bool QF16, bool MULTI>
-__global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
+template <int HDP, bool QF16, class A>
+__global__ __launch_bounds__(256) void decode_kernel(const A a) {
+    using T = decode_traits<A>;
+    constexpr bool MULTI = T::multi;
+    const decode_params& p = a.p;
     constexpr int NS = HDP / 32;   // k-steps of the score product
     constexpr int NT = HDP / 16;   // 16-dim tiles of the output
-    constexpr int SPAN = HDP / 4;  // dims a lane group holds across the k-steps
 
     const int tid = threadIdx.x;
     const int w = tid >> 6;
     const int ln = tid & 63;
     const int G = ln >> 4;  // lane group
     const int r = ln & 15;  // row / column inside the group
-    const uint32_t hd = a.hd;
-    const uint32_t group = a.group;
+    const uint32_t hd = p.hd;
+    const uint32_t group = p.group;
 
     // Block -> (sequence, split, KV head). Splits of one KV head are n_kv
     // blocks apart, so with n_kv a multiple of 8 they share an XCD (and its L2).
@@ -116,21 +140,21 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     // loads served last, so it must not be among them (measured: 0.9 us per
     // config-2 step). Partials sit at the split's own slot.
     const uint32_t b = blockIdx.x;
-    const uint32_t g = b % a.n_kv;
-    const uint32_t sb = b / a.n_kv;
-    const uint32_t si = find_seq<MULTI>(a.block0s, a.n_seqs, sb);
-    const decode_seq& s = a.seq[si];
+    const uint32_t g = b % p.n_kv;
+    const uint32_t sb = b / p.n_kv;
+    const uint32_t si = T::find(a, sb);
+    const decode_seq& s = T::seq(a, si);
     const uint32_t split = s.n_splits - 1 - (sb - s.block0);
-    const std::size_t slot = static_cast<std::size_t>(s.block0 + split) * a.n_kv + g;
-    const uint32_t t_begin = split * a.chunk;
-    const uint32_t t_end = min(s.len, t_begin + a.chunk);
+    const std::size_t slot = static_cast<std::size_t>(s.block0 + split) * p.n_kv + g;
+    const uint32_t t_begin = split * p.chunk;
+    const uint32_t t_end = min(s.len, t_begin + p.chunk);
     const uint32_t h0 = g * group;
-    const float c = a.scale_log2e;
+    const float c = p.scale_log2e;
     // The step's new row (position len-1) is in this block's split: take it
     // from k_new / v_new, rounded to binary16, and store it into the cache.
     const uint32_t new_t = s.len - 1;
     const bool new_here = s.k_new != nullptr && t_end == s.len;
-    const bool kv_f16 = a.kv_dtype == 1;
+    const bool kv_f16 = p.kv_dtype == 1;
 
     // Every K, V load below is unconditional, so a wave issues all of them
     // back to back: a lane with nothing to read points at valid data and
@@ -167,8 +191,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     // tb + 8G + 4e + i. V^T rows: lane (G, r) of tile n holds dim 16n + r at
     // positions tb + 8G + [0, 8). Both through buffer resources based at the
     // split: K past the split and dims past the head read as zeros.
-    _Float16* kbase = s.k + g * hd + G * SPAN;
-    const uint32_t row2 = a.row * 2;
+    _Float16* kbase = s.k + g * hd + 8 * G;
+    const uint32_t row2 = p.row * 2;
     const uint32_t vstride2 = s.ctx_stride * 2;
     // The new row's own cache slot is not read (the step overwrites it), nor
     // are V columns that start at or past it or the split end: those lanes
@@ -180,7 +204,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     // (readfirstlane: without it the batched kernel cannot tell the limit is
     // uniform and wraps every K load in a loop over lanes.)
     const uint32_t k_rows = __builtin_amdgcn_readfirstlane(min(t_end, s.len - (s.k_new != nullptr ? 1u : 0u)) - t_begin);
-    const rsrc k_res = make_rsrc(s.k + static_cast<std::size_t>(t_begin) * a.row + g * hd,
+    const rsrc k_res = make_rsrc(s.k + static_cast<std::size_t>(t_begin) * p.row + g * hd,
                                  k_rows ? k_rows * row2 - g * hd * 2 : 0u);
     const rsrc v_res = make_rsrc(s.vt + static_cast<std::size_t>(g) * hd * s.ctx_stride + t_begin,
                                  hd * vstride2 - t_begin * 2);
@@ -190,7 +214,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
             const uint32_t rel = tb - t_begin + 8 * (r >> 2) + 4 * e + (r & 3);
 #pragma unroll
             for (int st = 0; st < NS; ++st) {
-                const uint32_t d0 = G * SPAN + 8 * st;
+                const uint32_t d0 = 8 * G + 32 * st;
                 kr[e][st] = buffer_load16(k_res, d0 < hd ? rel * row2 + d0 * 2 : buffer_oob);
             }
         }
@@ -210,7 +234,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
     for (int n = 0; n < NT; ++n) {
         o[n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    // q^T operand: lane (G, r) holds head h0 + r, dims G*SPAN + 8*st + [0, 8),
+    // q^T operand: lane (G, r) holds head h0 + r, dims 32*st + 8*G + [0, 8),
     // rounded to binary16 as attend_group rounds q (S/kernels/attention.hpp:204-206).
     h8 qv[NS];
     const auto convert_q = [&](bool kv_issued) {
@@ -230,7 +254,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
         lds_barrier();
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            const uint32_t d0 = G * SPAN + 8 * st;
+            const uint32_t d0 = 8 * G + 32 * st;
             const uint32_t e0 = static_cast<uint32_t>(r) * hd + d0;
             if (static_cast<uint32_t>(r) < group && d0 < hd) {
                 if constexpr (QF16) {
@@ -257,10 +281,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
             for (int e = 0; e < 2; ++e) {
                 const uint32_t t = tb + 8 * (r >> 2) + 4 * e + (r & 3);
                 if (t == new_t) {
-                    _Float16* kp = kbase + static_cast<std::size_t>(t) * a.row;
+                    _Float16* kp = kbase + static_cast<std::size_t>(t) * p.row;
 #pragma unroll
                     for (int st = 0; st < NS; ++st) {
-                        const uint32_t d0 = G * SPAN + 8 * st;
+                        const uint32_t d0 = 8 * G + 32 * st;
                         if (d0 < hd) {
                             if (kv_f16) {
                                 kr[e][st] = *reinterpret_cast<const u4*>(new_lds + 2 * d0);
@@ -270,7 +294,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
                                 kr[e][st] = as_u4(h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]),
                                                      to_h(hi[0]), to_h(hi[1]), to_h(hi[2]), to_h(hi[3])});
                             }
-                            store16(kp + 8 * st, kr[e][st]);
+                            store16(kp + 32 * st, kr[e][st]);
                         }
                     }
                 }
@@ -401,10 +425,17 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
             }
         }
     }
-    __syncthreads();
+    // LDS only: the block appending the step's row must not wait here for
+    // its scattered cache stores, as __syncthreads() would.
+    lds_barrier();
 
+    // Every thread combines the waves for 4 consecutive elements of one head:
+    // the output for a sequence of one split, else this split's partial,
+    // which the merge kernel reads after the kernel boundary.
     const uint32_t nout = group * hd;
-    for (uint32_t e = tid; e < nout; e += 256) {
+    float* part_o = p.part + slot * nout;
+    float* part_ml = p.part + static_cast<std::size_t>(p.total_slots) * nout + slot * group * 2;
+    for (uint32_t e = 4 * tid; e < nout; e += 4 * 256) {
         const uint32_t h = e / hd;
         const uint32_t d = e % hd;
         float mw[4];
@@ -414,80 +445,93 @@ __global__ __launch_bounds__(256) void decode_kernel(const decode_args a) {
             mw[v] = lds_ml[(v * 16 + h) * 2];
             mx = fmaxf(mx, mw[v]);
         }
-        float sum = 0.0f, acc = 0.0f;
+        float sum = 0.0f;
+        f4 acc{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const float f = fast_exp2((mw[v] - mx) * c);  // 0 for a wave with no positions
             sum += lds_ml[(v * 16 + h) * 2 + 1] * f;
-            acc += lds_o[(v * group + h) * orow + d] * f;
+            acc += f * *reinterpret_cast<const f4*>(lds_o + (v * group + h) * orow + d);
         }
         if (s.n_splits == 1) {
-            s.out[static_cast<std::size_t>(h0) * hd + e] = acc / sum;
+            *reinterpret_cast<f4*>(s.out + static_cast<std::size_t>(h0) * hd + e) = acc / sum;
         } else {
-            // This split's partial; the merge kernel combines them.
-            a.part_o[slot * nout + e] = acc;
+            *reinterpret_cast<f4*>(part_o + e) = acc;
             if (d == 0) {
-                a.part_ml[(slot * group + h) * 2] = mx;
-                a.part_ml[(slot * group + h) * 2 + 1] = sum;
+                part_ml[2 * h] = mx;
+                part_ml[2 * h + 1] = sum;
             }
         }
     }
 }
 
 // One block per (sequence with splits, query head): out = sum_j w_j O_j with
-// w_j = exp2((m_j - max) c) / sum_i l_i exp2((m_i - max) c).
-template <bool MULTI>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const decode_args a) {
+// w_j = exp2((m_j - max) c) / sum_i l_i exp2((m_i - max) c), splits in a
+// fixed order, so results are deterministic.
+//
+// Every load is unconditional and issued before any is used: lanes with
+// nothing to read take an out-of-range buffer offset and get zeros. (Loads
+// guarded by a condition into an array were issued one at a time, each
+// waited for before the next: eight round trips instead of one.)
+template <class A>
+__global__ __launch_bounds__(256) void decode_merge_kernel(const A a) {
+    using T = decode_traits<A>;
+    const decode_params& p = a.p;
     __shared__ float wts[decode_max_splits];
     __shared__ f4 acc_lds[256];
     const int tid = threadIdx.x;
     const int ln = tid & 63;
     const uint32_t u = blockIdx.x;
-    const uint32_t si = find_seq<MULTI>(a.merge0s, a.n_seqs, u);
-    const decode_seq& s = a.seq[si];
+    const uint32_t si = T::find_merge(a, u);
+    const decode_seq& s = T::seq(a, si);
     // Heads of one KV head go n_kv blocks apart, as the split kernel's
     // blocks do, so with n_kv a multiple of 8 a merge block runs on the XCD
     // whose L2 took its KV head's partials.
     const uint32_t k = u - s.merge0;
-    const uint32_t g = k % a.n_kv;
-    const uint32_t h = k / a.n_kv;
-    const uint32_t hd = a.hd;
-    const uint32_t nout = a.group * hd;
+    const uint32_t g = k % p.n_kv;
+    const uint32_t h = k / p.n_kv;
+    const uint32_t hd = p.hd;
+    const uint32_t group = p.group;
+    const uint32_t nout = group * hd;
     const uint32_t S = s.n_splits;
-    const float c = a.scale_log2e;
-    const auto pblock = [&](uint32_t j) { return static_cast<std::size_t>(s.block0 + j) * a.n_kv + g; };
+    const float c = p.scale_log2e;
+    // Partials of this (sequence, KV head): split j's O at slot (block0 + j) * n_kv + g.
+    const uint32_t o_stride = p.n_kv * nout * 4;   // bytes between consecutive splits' O
+    const uint32_t ml_stride = p.n_kv * group * 8;  // and (max, sum) pairs
+    const std::size_t slot0 = static_cast<std::size_t>(s.block0) * p.n_kv + g;
+    const rsrc o_r = make_rsrc(p.part + slot0 * nout + static_cast<std::size_t>(h) * hd, (S - 1) * o_stride + hd * 4);
+    const rsrc ml_r = make_rsrc(p.part + static_cast<std::size_t>(p.total_slots) * nout + (slot0 * group + h) * 2,
+                                (S - 1) * ml_stride + 8);
 
     // The head's hd/4 output quads times P parts of the splits fill the
-    // block. The first 8 partial outputs of every thread are loaded before
-    // the weights are known, so both loads overlap.
+    // block; the first 8 partial outputs of every thread go out before the
+    // weights are known.
     const uint32_t nq = hd / 4;
     const uint32_t P = 256 / nq;
     const uint32_t q = tid % nq;
     const uint32_t part = tid / nq;
-    const float* src = a.part_o + static_cast<std::size_t>(h) * hd + 4 * q;
+    const auto o_off = [&](uint32_t j) { return part < P && j < S ? j * o_stride + 16 * q : buffer_oob; };
     f4 ov[8];
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t j = part + i * P;
-        if (part < P && j < S) {
-            ov[i] = *reinterpret_cast<const f4*>(src + pblock(j) * nout);
-        }
+        ov[i] = __builtin_bit_cast(f4, buffer_load16(o_r, o_off(part + i * P)));
     }
 
     // Phase 1 (wave 0): lane l holds splits l, l + 64, ...
     if (tid < 64) {
         constexpr uint32_t per_lane = decode_max_splits / 64;
         float mj[per_lane], lj[per_lane];
-        float mx = -INFINITY;
 #pragma unroll
         for (uint32_t i = 0; i < per_lane; ++i) {
             const uint32_t j = ln + 64 * i;
-            mj[i] = -INFINITY;
-            lj[i] = 0.0f;
-            if (j < S) {
-                mj[i] = a.part_ml[(pblock(j) * a.group + h) * 2];
-                lj[i] = a.part_ml[(pblock(j) * a.group + h) * 2 + 1];
-            }
+            const uint32_t off = j < S ? j * ml_stride : buffer_oob;
+            mj[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_r, off, 0, 0));
+            lj[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_r, off == buffer_oob ? off : off + 4, 0, 0));
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (uint32_t i = 0; i < per_lane; ++i) {
+            mj[i] = ln + 64 * i < S ? mj[i] : -INFINITY;
             mx = fmaxf(mx, mj[i]);
         }
         mx = wave_max(mx);
@@ -509,29 +553,27 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const decode_args a) 
     }
     __syncthreads();
     // Phase 2: out = sum_j w_j O_j, splits in a fixed order per thread.
-    if (part < P) {
-        f4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t j = part + i * P;
+        if (part < P && j < S) {
+            acc += wts[j] * ov[i];
+        }
+    }
+    for (uint32_t j = part + 8 * P; j < S; j += 8 * P) {
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
-            const uint32_t j = part + i * P;
-            if (j < S) {
-                acc += wts[j] * ov[i];
+            ov[i] = __builtin_bit_cast(f4, buffer_load16(o_r, o_off(j + i * P)));
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            if (part < P && j + i * P < S) {
+                acc += wts[j + i * P] * ov[i];
             }
         }
-        for (uint32_t j = part + 8 * P; j < S; j += 8 * P) {
-#pragma unroll
-            for (uint32_t i = 0; i < 8; ++i) {
-                if (j + i * P < S) {
-                    ov[i] = *reinterpret_cast<const f4*>(src + pblock(j + i * P) * nout);
-                }
-            }
-#pragma unroll
-            for (uint32_t i = 0; i < 8; ++i) {
-                if (j + i * P < S) {
-                    acc += wts[j + i * P] * ov[i];
-                }
-            }
-        }
+    }
+    if (part < P) {
         acc_lds[part * nq + q] = acc;
     }
     __syncthreads();
@@ -540,29 +582,47 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const decode_args a) 
         for (uint32_t p2 = 1; p2 < P; ++p2) {
             sum += acc_lds[p2 * nq + tid];
         }
-        *reinterpret_cast<f4*>(s.out + (static_cast<std::size_t>(g) * a.group + h) * hd + 4 * tid) = sum;
+        *reinterpret_cast<f4*>(s.out + (static_cast<std::size_t>(g) * group + h) * hd + 4 * tid) = sum;
     }
 }
 
-template <int HDP, bool MULTI>
-hipError_t launch_hdp(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream) {
-    const std::size_t lds = decode_lds_bytes(a.group, a.hd);
-    const dim3 grid(total_splits * a.n_kv);
+template <int HDP, class A>
+hipError_t launch_hdp(const A& a, uint32_t q_dtype, hipStream_t stream) {
+    const std::size_t lds = decode_lds_bytes(a.p.group, a.p.hd);
+    const dim3 grid(a.p.total_slots);
     if (q_dtype == 1) {
-        decode_kernel<HDP, true, MULTI><<<grid, 256, lds, stream>>>(a);
+        decode_kernel<HDP, true, A><<<grid, 256, lds, stream>>>(a);
     } else {
-        decode_kernel<HDP, false, MULTI><<<grid, 256, lds, stream>>>(a);
+        decode_kernel<HDP, false, A><<<grid, 256, lds, stream>>>(a);
     }
-    if (a.merge_blocks > 0) {
-        decode_merge_kernel<MULTI><<<a.merge_blocks, 256, 0, stream>>>(a);
+    if (a.p.merge_blocks > 0) {
+        decode_merge_kernel<A><<<a.p.merge_blocks, 256, 0, stream>>>(a);
     }
     return hipGetLastError();
 }
 
-template <int HDP>
-hipError_t launch_hdp(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream) {
-    return a.n_seqs > 1 ? launch_hdp<HDP, true>(a, total_splits, q_dtype, stream)
-                        : launch_hdp<HDP, false>(a, total_splits, q_dtype, stream);
+template <class A>
+hipError_t launch_any(const A& a, uint32_t q_dtype, hipStream_t stream) {
+    switch ((a.p.hd + 31) / 32 * 32) {
+    case 32:
+        return launch_hdp<32>(a, q_dtype, stream);
+    case 64:
+        return launch_hdp<64>(a, q_dtype, stream);
+    case 96:
+        return launch_hdp<96>(a, q_dtype, stream);
+    case 128:
+        return launch_hdp<128>(a, q_dtype, stream);
+    case 160:
+        return launch_hdp<160>(a, q_dtype, stream);
+    case 192:
+        return launch_hdp<192>(a, q_dtype, stream);
+    case 224:
+        return launch_hdp<224>(a, q_dtype, stream);
+    case 256:
+        return launch_hdp<256>(a, q_dtype, stream);
+    default:
+        return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
@@ -580,28 +640,12 @@ uint32_t decode_choose_chunk(uint64_t total_positions, uint32_t n_kv, uint32_t m
     return static_cast<uint32_t>(chunk);
 }
 
-hipError_t launch_decode(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream) {
-    const uint32_t hdp = (a.hd + 31) / 32 * 32;
-    switch (hdp) {
-    case 32:
-        return launch_hdp<32>(a, total_splits, q_dtype, stream);
-    case 64:
-        return launch_hdp<64>(a, total_splits, q_dtype, stream);
-    case 96:
-        return launch_hdp<96>(a, total_splits, q_dtype, stream);
-    case 128:
-        return launch_hdp<128>(a, total_splits, q_dtype, stream);
-    case 160:
-        return launch_hdp<160>(a, total_splits, q_dtype, stream);
-    case 192:
-        return launch_hdp<192>(a, total_splits, q_dtype, stream);
-    case 224:
-        return launch_hdp<224>(a, total_splits, q_dtype, stream);
-    case 256:
-        return launch_hdp<256>(a, total_splits, q_dtype, stream);
-    default:
-        return hipErrorInvalidValue;
-    }
+hipError_t launch_decode(const decode_one_args& a, uint32_t q_dtype, hipStream_t stream) {
+    return launch_any(a, q_dtype, stream);
+}
+
+hipError_t launch_decode(const decode_batch_args& a, uint32_t q_dtype, hipStream_t stream) {
+    return launch_any(a, q_dtype, stream);
 }
 
 }  // namespace syn

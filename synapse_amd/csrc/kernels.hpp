@@ -37,27 +37,44 @@ struct decode_seq {
     uint32_t merge0;      // first merge block of this sequence (sequences with one split have none)
 };
 
-constexpr uint32_t decode_max_seqs = 32;  // sequences per launch (kernel-argument table)
+constexpr uint32_t decode_max_seqs = 32;  // sequences per batched launch (kernel-argument table)
 constexpr uint32_t decode_positions_per_wave = 32;
 constexpr uint32_t decode_waves = 4;
 constexpr uint32_t decode_chunk_unit = decode_positions_per_wave * decode_waves;  // 128
-constexpr uint32_t decode_max_splits = 256;  // splits of one sequence (bounds the merge's LDS)
+constexpr uint32_t decode_max_splits = 256;  // splits of one sequence
 
-struct decode_args {
-    decode_seq seq[decode_max_seqs];
-    uint32_t block0s[decode_max_seqs];  // seq[i].block0, contiguous: a block finds its sequence in one load batch
-    uint32_t merge0s[decode_max_seqs];  // seq[i].merge0, likewise for the merge kernel
-    uint32_t n_seqs;
+// The splits of a sequence are combined by a second, small kernel on the same
+// stream: one block per (sequence with splits, query head). (Merging inside
+// the split kernel, through arrival counters and agent-scope loads, measured
+// slower: each cross-block hop costs a loaded memory round trip, and the
+// merge needs three or four of them.)
+struct decode_params {
+    float* part;           // partial O [slots][group][hd], then (max, sum) [slots][group][2]; slot = split * n_kv + g
     uint32_t n_kv;
     uint32_t hd;
     uint32_t group;        // query heads per KV head, <= 16
     uint32_t row;          // n_kv * hd: K row length in halves
     uint32_t chunk;        // positions per split, a multiple of decode_chunk_unit
     uint32_t kv_dtype;     // type of k_new / v_new: 0 f32, 1 f16
-    uint32_t merge_blocks; // blocks of the merge kernel: one per (split sequence, query head)
+    uint32_t total_slots;  // split blocks of the launch: splits * n_kv
+    uint32_t merge_blocks; // blocks of the merge kernel: n_kv * group per sequence with splits
+    uint32_t n_seqs;
     float scale_log2e;     // scale * log2(e)
-    float* part_o;         // [splits * n_kv][group][hd]
-    float* part_ml;        // [splits * n_kv][group][2]
+};
+
+// One sequence: the argument block a decode step carries (~120 bytes; a
+// kernel-argument block of kilobytes costs a microsecond per launch).
+struct decode_one_args {
+    decode_params p;
+    decode_seq s;
+};
+
+// Up to decode_max_seqs sequences in one launch (ragged batched decode).
+struct decode_batch_args {
+    decode_params p;
+    decode_seq seq[decode_max_seqs];
+    uint32_t block0s[decode_max_seqs];  // seq[i].block0, contiguous: a block finds its sequence in one load batch
+    uint32_t merge0s[decode_max_seqs];  // seq[i].merge0, likewise for the merge kernel
 };
 
 // Scratch floats one split contributes: (max, sum, output) for each head.
@@ -75,7 +92,8 @@ inline bool decode_fits(uint32_t chunk, uint32_t row, uint32_t hd, uint32_t ctx_
     return uint64_t{chunk} * row * 2 < (uint64_t{1} << 31) && uint64_t{hd} * ctx_stride * 2 < (uint64_t{1} << 31);
 }
 
-hipError_t launch_decode(const decode_args& a, uint32_t total_splits, uint32_t q_dtype, hipStream_t stream);
+hipError_t launch_decode(const decode_one_args& a, uint32_t q_dtype, hipStream_t stream);
+hipError_t launch_decode(const decode_batch_args& a, uint32_t q_dtype, hipStream_t stream);
 
 // ---- flash prefill / bidirectional -----------------------------------------
 struct flash_args {

@@ -192,3 +192,4 @@ def test_decode_step_with_f16_rows(arena, ctx):
     ok_k[:ctx], ok_v[:ctx] = kc, vc
     want = orc.attention_rows(q, k, v, ctx, ok_k, ok_v, n_heads, cfg.scale)
     assert_close(outs[1], want, what=f"f16 rows ctx {ctx}")
+

@@ -125,6 +125,19 @@ uint64_t syn_hip_attention_scratch_bytes(uint32_t n_heads, uint32_t n_kv_heads, 
  * attention, :254-269). Softmax and accumulation in f32, f32 output. */
 int syn_hip_attention(syn_arena* arena, const syn_attn_desc* desc);
 
+/* No reference counterpart: syn_hip_attention for callers that cannot let a
+ * call allocate or take caller scratch -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation. Same inputs,
+ * outputs and results; desc's scratch_offset / scratch_bytes are ignored.
+ * The split-KV decode's partials go to a file-scope device array of
+ * syn_hip_attention_noalloc_scratch_limit() bytes (4 MiB) that each GPU holds
+ * until the process ends; a step whose partials need more returns
+ * SYN_HIP_EINVAL without launching. Every call on one GPU shares that array:
+ * calls that overlap on one GPU (different streams or arenas) race. Nothing
+ * in the array needs to start at zero. */
+int syn_hip_attention_noalloc(syn_arena* arena, const syn_attn_desc* desc);
+uint64_t syn_hip_attention_noalloc_scratch_limit(void);
+
 /* The attend half only: the cache already holds rows 0..pos+n-1 (desc's
  * k_offset and v_offset are ignored). */
 int syn_hip_attend(syn_arena* arena, const syn_attn_desc* desc);

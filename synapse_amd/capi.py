@@ -107,6 +107,8 @@ SIGNATURES = {
     "syn_hip_attention_scratch_bytes": (u64, [u32, u32, u32, u32, u32]),
     "syn_hip_attention": (i32, [ctypes.c_void_p, ctypes.POINTER(AttnDesc)]),
     "syn_hip_attend": (i32, [ctypes.c_void_p, ctypes.POINTER(AttnDesc)]),
+    "syn_hip_attention_noalloc": (i32, [ctypes.c_void_p, ctypes.POINTER(AttnDesc)]),
+    "syn_hip_attention_noalloc_scratch_limit": (u64, []),
     "syn_hip_kv_append": (i32, [ctypes.c_void_p, ctypes.POINTER(KvDesc), u64, u64, u32, u32, u32]),
     "syn_hip_attend_batch_scratch_bytes": (u64, [ctypes.POINTER(SeqDesc), u32, u32]),
     "syn_hip_attend_batch": (i32, [ctypes.c_void_p, ctypes.POINTER(SeqDesc), u32, u32, f32, u32, u64, u64]),

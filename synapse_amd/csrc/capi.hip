@@ -13,6 +13,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 struct syn_arena {
@@ -22,9 +23,24 @@ struct syn_arena {
     int device = 0;
 };
 
+// ---- the allocation-free entry point's scratch ------------------------------
+// syn_hip_attention_noalloc keeps the split-KV decode's partials here instead
+// of in caller scratch: 4 MiB per device, held until the process ends (e.g.
+// config 2, 33 splits x 8 KV heads x 4 heads x 130 floats, takes 549 KB).
+// In host code `scratch` names a host-side stand-in; kernels get the device
+// address that hipGetSymbolAddress returns for the current device.
+constexpr std::size_t noalloc_scratch_bytes = std::size_t{4} << 20;
+static __device__ __align__(256) float scratch[noalloc_scratch_bytes / sizeof(float)];
+
 namespace {
 
 constexpr uint64_t no_offset = ~uint64_t{0};
+
+// Device address of `scratch`, one per device (each device holds its own copy
+// of the array at its own address), looked up with that device current.
+constexpr int max_devices = 64;
+std::mutex scratch_mutex;
+float* scratch_device[max_devices] = {};
 
 thread_local char last_error[512] = "";
 
@@ -42,6 +58,23 @@ int hip_status(hipError_t e, const char* what) {
         return SYN_HIP_OK;
     }
     return fail(static_cast<int>(e), "%s: %s", what, hipGetErrorString(e));
+}
+
+// Looks up (once per device) the static scratch's address on `device`, which
+// must be the current device.
+int lookup_scratch(int device) {
+    if (device < 0 || device >= max_devices) {
+        return fail(SYN_HIP_ENODEV, "device %d: no static scratch slot", device);
+    }
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (scratch_device[device] == nullptr) {
+        void* ptr = nullptr;
+        if (int e = hip_status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) {
+            return e;
+        }
+        scratch_device[device] = static_cast<float*>(ptr);
+    }
+    return SYN_HIP_OK;
 }
 
 // [offset, offset + bytes) inside the arena, without wrapping.
@@ -124,10 +157,18 @@ uint64_t decode_scratch_bytes(uint32_t splits, uint32_t n_kv, uint32_t group, ui
     return uint64_t{splits} * n_kv * syn::decode_split_floats(group, hd) * sizeof(float);
 }
 
+// Where a decode launch keeps its split partials: caller scratch in the arena
+// (checked against it), or the library's static array (`device` non-null).
+struct partial_area {
+    uint64_t arena_offset;
+    uint64_t bytes;
+    float* device;
+};
+
 // One decode launch over seqs[0..n): fills the argument block, checks the
 // scratch, launches. kv_dtype types the sequences' k_new / v_new rows.
 int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n_kv, uint32_t hd, uint32_t group,
-               float scale, uint32_t q_dtype, uint32_t kv_dtype, uint64_t scratch_offset, uint64_t scratch_bytes) {
+               float scale, uint32_t q_dtype, uint32_t kv_dtype, const partial_area& pa) {
     if (n == 0 || n > syn::decode_max_seqs) {
         return fail(SYN_HIP_EINVAL, "decode: %u sequences in one launch", n);
     }
@@ -169,14 +210,23 @@ int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n
     prm.scale_log2e = scale * syn::log2e;
     if (merge_blocks > 0) {
         const uint64_t need = decode_scratch_bytes(splits, n_kv, group, hd);
-        if (need > scratch_bytes) {
+        if (need > pa.bytes) {
+            if (pa.device != nullptr) {
+                return fail(SYN_HIP_EINVAL, "decode: the allocation-free entry point's static scratch holds %llu "
+                            "bytes; this step's split partials need %llu",
+                            static_cast<unsigned long long>(pa.bytes), static_cast<unsigned long long>(need));
+            }
             return fail(SYN_HIP_EINVAL, "decode: scratch of %llu bytes, %llu needed",
-                        static_cast<unsigned long long>(scratch_bytes), static_cast<unsigned long long>(need));
+                        static_cast<unsigned long long>(pa.bytes), static_cast<unsigned long long>(need));
         }
-        if (int e = check_range(a, scratch_offset, need, 16, "decode scratch")) {
-            return e;
+        if (pa.device != nullptr) {
+            prm.part = pa.device;
+        } else {
+            if (int e = check_range(a, pa.arena_offset, need, 16, "decode scratch")) {
+                return e;
+            }
+            prm.part = reinterpret_cast<float*>(a->base + pa.arena_offset);
         }
-        prm.part = reinterpret_cast<float*>(a->base + scratch_offset);
     }
     if (n == 1) {
         syn::decode_one_args one{prm, table[0]};
@@ -267,7 +317,7 @@ bool decode_shape(const syn_attn_desc* d) {
 
 // Attends the run; with_new_rows, a single-token step's K, V row is appended
 // by the decode kernel itself (one launch), longer runs were appended before.
-int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows) {
+int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows, const partial_area* static_area = nullptr) {
     const syn_kv_desc& c = d->cache;
     const uint32_t group = d->n_heads / c.n_kv_heads;
     if (decode_shape(d)) {
@@ -282,8 +332,9 @@ int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows) {
         }
         s.len = d->pos + 1;
         s.ctx_stride = c.ctx_stride;
+        const partial_area arena_area{d->scratch_offset, d->scratch_bytes, nullptr};
         return run_decode(a, &s, 1, c.n_kv_heads, c.head_dim, group, d->scale, d->q_dtype, d->kv_dtype,
-                          d->scratch_offset, d->scratch_bytes);
+                          static_area != nullptr ? *static_area : arena_area);
     }
     const syn::flash_args f = flash_of(a, d);
     if (fast_shape(c.head_dim) && (uint64_t{d->n} + 127) / 128 <= 65535 &&
@@ -352,6 +403,11 @@ int syn_hip_arena_create(size_t bytes, syn_arena** out) {
     a->base = static_cast<char*>(p);
     a->bytes = bytes;
     a->device = device;
+    if (int e = lookup_scratch(device)) {
+        (void)hipFree(p);
+        delete a;
+        return e;
+    }
     if (hipStreamCreateWithFlags(&a->stream, hipStreamNonBlocking) != hipSuccess) {
         (void)hipFree(p);
         delete a;
@@ -517,6 +573,27 @@ int syn_hip_attention(syn_arena* a, const syn_attn_desc* d) {
     return attend_checked(a, d, false);
 }
 
+int syn_hip_attention_noalloc(syn_arena* a, const syn_attn_desc* d) {
+    if (int e = check_attn(a, d, true)) {
+        return e;
+    }
+    if (!decode_shape(d)) {
+        // Runs of more than one token (and shapes outside the split-KV
+        // kernel) use no scratch: the same launches as syn_hip_attention.
+        return syn_hip_attention(a, d);
+    }
+    float* dev = scratch_device[a->device];
+    if (dev == nullptr) {
+        return fail(SYN_HIP_ENODEV, "static scratch of device %d was not looked up", a->device);
+    }
+    const partial_area area{0, noalloc_scratch_bytes, dev};
+    return attend_checked(a, d, true, &area);
+}
+
+uint64_t syn_hip_attention_noalloc_scratch_limit(void) {
+    return noalloc_scratch_bytes;
+}
+
 int syn_hip_attend(syn_arena* a, const syn_attn_desc* d) {
     if (int e = check_attn(a, d, false)) {
         return e;
@@ -634,7 +711,8 @@ int syn_hip_attend_batch(syn_arena* a, const syn_seq_desc* seqs, uint32_t n_seqs
             ds[i].len = s.pos + 1;
             ds[i].ctx_stride = s.cache.ctx_stride;
         }
-        if (int e = run_decode(a, ds, nb, n_kv, hd, group, scale, q_dtype, SYN_F32, scratch_offset, scratch_bytes)) {
+        if (int e = run_decode(a, ds, nb, n_kv, hd, group, scale, q_dtype, SYN_F32,
+                               partial_area{scratch_offset, scratch_bytes, nullptr})) {
             return e;
         }
     }

@@ -360,6 +360,30 @@ private:
 
 class graph_builder;
 
+// A tensor's row layout: floats per row, whether it has a row per run row
+// (batched) or a single row, and how many run rows share one of its rows
+// (row_div: 1, or s*s below a pixel_shuffle).
+struct row_layout {
+    std::size_t size = 0;
+    bool batched = true;
+    std::size_t row_div = 1;
+
+    static constexpr row_layout per_run_row(std::size_t size) noexcept {
+        return {size, true, 1};
+    }
+    static constexpr row_layout one_row(std::size_t size) noexcept {
+        return {size, false, 1};
+    }
+    constexpr row_layout with_size(std::size_t s) const noexcept {
+        return {s, batched, row_div};
+    }
+    // What per-token operations take (I8).
+    constexpr bool per_token() const noexcept {
+        return batched && row_div == 1;
+    }
+    constexpr bool operator==(const row_layout&) const = default;
+};
+
 class compute_graph {
 public:
     const std::vector<tensor_desc>& tensors() const noexcept {
@@ -377,514 +401,529 @@ public:
     const std::vector<tensor_id>& outputs() const noexcept {
         return outputs_;
     }
-    // Positions a run accepts are < position_limit(): the smallest KV cache's max_ctx.
+    // A run's positions stay below this: the smallest KV cache's max_ctx.
     std::size_t position_limit() const noexcept {
-        return position_limit_;
+        return limits_.positions;
     }
     std::size_t max_batch() const noexcept {
-        return max_batch_;
+        return limits_.batch;
     }
-    // Tokens a run accepts are < token_limit(): the smallest embedding
-    // table's row count (unbounded without an embed node).
+    // A run's tokens stay below this: the smallest embedding table's row
+    // count (unbounded without an embed node).
     std::size_t token_limit() const noexcept {
-        return token_limit_;
+        return limits_.tokens;
     }
-    // True if every run must process exactly max_batch() rows (a pixel_shuffle, I9).
+    // Every run processes exactly max_batch() rows (the graph has a pixel_shuffle, I9).
     bool full_batch_only() const noexcept {
-        return full_batch_only_;
+        return limits_.whole_batches;
     }
-    // True if the graph has an embed node, so a run needs tokens.
+    // A run needs tokens (the graph has an embed node).
     bool embeds() const noexcept {
-        return embeds_;
+        return limits_.takes_tokens;
     }
-    // Rows a tensor holds: max_batch() / row_div if batched, else 1.
+    // Rows of tensor t: max_batch() / row_div when batched, else one.
     std::size_t rows(tensor_id t) const noexcept {
-        return tensors_[t].batched ? max_batch_ / tensors_[t].row_div : 1;
+        const tensor_desc& d = tensors_[t];
+        return d.batched ? limits_.batch / d.row_div : 1;
     }
 
 private:
     friend class graph_builder;
+    struct run_limits {
+        std::size_t batch = 1;
+        std::size_t positions = std::numeric_limits<std::size_t>::max();
+        std::size_t tokens = std::numeric_limits<std::size_t>::max();
+        bool whole_batches = false;
+        bool takes_tokens = false;
+    };
     compute_graph() = default;
     std::vector<tensor_desc> tensors_;
     std::vector<state_desc> states_;
     std::vector<node> nodes_;
     std::vector<tensor_id> inputs_;
     std::vector<tensor_id> outputs_;
-    std::size_t position_limit_ = std::numeric_limits<std::size_t>::max();
-    std::size_t token_limit_ = std::numeric_limits<std::size_t>::max();
-    std::size_t max_batch_ = 1;
-    bool full_batch_only_ = false;
-    bool embeds_ = false;
+    run_limits limits_;
 };
 
-// Builds a graph one operation at a time; after the first error every call
-// returns the invalid id and finalize() reports that error.
+// Builds a graph one operation at a time. Each operation validates its
+// operand ids, then applies its own shape and parameter rules in a fixed
+// order (so a misuse reports the reference's code), then sizes its result
+// (and scratch) against the byte budget (I5). The first failure latches:
+// every later call returns the invalid id, and finalize() reports the code
+// with the index of the node that was being added.
 class graph_builder {
 public:
+    // Rule: max_batch >= 1 (bad_shape). A batch too large for any tensor
+    // fails later, at the first tensor (too_large).
     explicit graph_builder(std::size_t max_batch = 1) {
-        if (max_batch == 0 || max_batch > std::numeric_limits<std::uint32_t>::max()) {
-            fail(graph_errc::bad_shape);
+        if (max_batch == 0) {
+            latch_.set(graph_errc::bad_shape, 0);
         } else {
-            g_.max_batch_ = max_batch;
+            graph_.limits_.batch = max_batch;
         }
     }
 
-    // A graph input of `size` floats per token (batched).
+    // A graph input of `size` floats per run row.
     tensor_id input(std::size_t size) {
-        if (failed()) {
+        if (latch_.set_already()) {
             return invalid_tensor;
         }
         if (size == 0) {
-            return fail(graph_errc::empty_tensor);
+            return reject(graph_errc::empty_tensor);
         }
-        const tensor_id t = add_floats(size, tensor_role::input);
+        const tensor_id t = new_rows(row_layout::per_run_row(size), tensor_role::input);
         if (t != invalid_tensor) {
-            g_.inputs_.push_back(t);
+            graph_.inputs_.push_back(t);
         }
         return t;
     }
 
-    // w * x (S/graph/graph.hpp:536-572). Pre (checked): x.size == cols(w);
-    // w in a format the device computes with.
+    // w * x for every row of x (S/graph/graph.hpp:536-572). Rules: x has
+    // cols(w) floats; w is in a format the device computes with. Block-format
+    // weights take their activations quantized once per run, into a scratch
+    // the library sizes (syn_hip_matmul_q_act_bytes).
     tensor_id matmul(const matrix_ref& w, tensor_id x) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (size_of(x) != cols(w)) {
-            return fail(graph_errc::size_mismatch);
-        }
-        if (!matrix_ok(w)) {
-            return fail(graph_errc::bad_parameter);
-        }
-        // Quantized weights take their activations quantized once per run,
-        // into this scratch (syn_hip_matmul_q_act_bytes for every row of x).
-        const std::size_t n = g_.rows(x);
-        std::size_t scratch_bytes = 1;
-        if (type_of(w) != SYN_TYPE_F32) {
-            if (n > std::numeric_limits<std::uint32_t>::max() || cols(w) > std::numeric_limits<std::uint32_t>::max()) {
-                return fail(graph_errc::too_large);
-            }
-            scratch_bytes = syn_hip_matmul_q_act_bytes(type_of(w), static_cast<std::uint32_t>(n),
-                                                       static_cast<std::uint32_t>(cols(w)));
-        }
-        const tensor_id out = add_floats(rows(w), tensor_role::intermediate, batched(x), row_div(x));
-        const tensor_id scratch = add_tensor(scratch_bytes, 0, tensor_role::scratch, false);
-        if (out == invalid_tensor || scratch == invalid_tensor) {
-            return invalid_tensor;
-        }
-        g_.nodes_.emplace_back(op_matmul{w, x, out, scratch});
-        return out;
+        return emit(
+            {x},
+            [&]() -> finding {
+                if (shape(x).size != cols(w)) {
+                    return graph_errc::size_mismatch;
+                }
+                return device_matrix(w) ? ok : finding{graph_errc::bad_parameter};
+            },
+            [&] { return shape(x).with_size(rows(w)); },
+            [&](tensor_id out, tensor_id scratch) { return op_matmul{w, x, out, scratch}; },
+            [&]() -> std::optional<std::size_t> {
+                if (type_of(w) == SYN_TYPE_F32) {
+                    return std::size_t{1};
+                }
+                const std::size_t n = graph_.rows(x);
+                if (n > std::numeric_limits<std::uint32_t>::max() || cols(w) > std::numeric_limits<std::uint32_t>::max()) {
+                    return std::nullopt;
+                }
+                return static_cast<std::size_t>(syn_hip_matmul_q_act_bytes(
+                    type_of(w), static_cast<std::uint32_t>(n), static_cast<std::uint32_t>(cols(w))));
+            });
     }
 
     tensor_id add(tensor_id a, tensor_id b) {
-        return binary<op_add>(a, b);
+        return elementwise2(a, b, [](tensor_id x, tensor_id y, tensor_id out) { return op_add{x, y, out}; });
     }
     tensor_id mul(tensor_id a, tensor_id b) {
-        return binary<op_mul>(a, b);
+        return elementwise2(a, b, [](tensor_id x, tensor_id y, tensor_id out) { return op_mul{x, y, out}; });
     }
 
-    // x + bias on every row. Pre (checked): bias is 1 x x.size (I2).
+    // x + bias on every row. Rule: bias is a 1 x size float vector (I2).
     tensor_id add_bias(tensor_id x, const matrix_ref& bias) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (rows(bias) != 1 || cols(bias) != size_of(x)) {
-            return fail(graph_errc::size_mismatch);
-        }
-        if (!vector_ok(bias)) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, batched(x), row_div(x));
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_add_bias{x, bias, out});
-        }
-        return out;
+        return emit(
+            {x}, [&] { return vector_rule(bias, shape(x).size); }, [&] { return shape(x); },
+            [&](tensor_id out) { return op_add_bias{x, bias, out}; });
     }
     tensor_id silu(tensor_id x) {
-        return unary<op_silu>(x);
+        return elementwise1(x, [](tensor_id in, tensor_id out) { return op_silu{in, out}; });
     }
     tensor_id softmax(tensor_id x) {
-        return unary<op_softmax>(x);
+        return elementwise1(x, [](tensor_id in, tensor_id out) { return op_softmax{in, out}; });
+    }
+    tensor_id gelu(tensor_id x) {
+        return elementwise1(x, [](tensor_id in, tensor_id out) { return op_gelu{in, out}; });
     }
 
-    // x / rms(x) * gamma. Pre (checked): gamma is 1 x x.size.
+    // x / rms(x) * gamma. Rule: gamma is a 1 x size float vector.
     tensor_id rms_norm(tensor_id x, const matrix_ref& gamma, float eps) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (rows(gamma) != 1 || cols(gamma) != size_of(x)) {
-            return fail(graph_errc::size_mismatch);
-        }
-        if (!vector_ok(gamma)) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, batched(x), row_div(x));
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_rms_norm{x, gamma, eps, out});
-        }
-        return out;
+        return emit(
+            {x}, [&] { return vector_rule(gamma, shape(x).size); }, [&] { return shape(x); },
+            [&](tensor_id out) { return op_rms_norm{x, gamma, eps, out}; });
     }
 
-    // Row `token` of table for each token of a run. Pre (checked): table non-empty.
+    // Row `token` of table for each token of a run. Rule: the table is
+    // non-empty, in a device format, with at most 2^32 - 1 rows.
     tensor_id embed(const matrix_ref& table) {
-        if (failed()) {
-            return invalid_tensor;
-        }
-        if (rows(table) == 0 || cols(table) == 0) {
-            return fail(graph_errc::empty_tensor);
-        }
-        if (!matrix_ok(table) || rows(table) > std::numeric_limits<std::uint32_t>::max()) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(cols(table), tensor_role::intermediate, true);
-        if (out != invalid_tensor) {
-            g_.token_limit_ = std::min(g_.token_limit_, rows(table));
-            g_.embeds_ = true;
-            g_.nodes_.emplace_back(op_embed{table, out});
-        }
-        return out;
+        return emit(
+            {},
+            [&]() -> finding {
+                if (rows(table) == 0 || cols(table) == 0) {
+                    return graph_errc::empty_tensor;
+                }
+                if (!device_matrix(table) || rows(table) > std::numeric_limits<std::uint32_t>::max()) {
+                    return graph_errc::bad_parameter;
+                }
+                return ok;
+            },
+            [&] { return row_layout::per_run_row(cols(table)); },
+            [&](tensor_id out) {
+                graph_.limits_.tokens = std::min(graph_.limits_.tokens, rows(table));
+                graph_.limits_.takes_tokens = true;
+                return op_embed{table, out};
+            });
     }
 
     // Every head of x rotated by its token's position, theta_i = pos *
     // base^(-2i / head_dim) / freq_factors[i] (S/graph/graph.hpp:642-676,
-    // S/kernels/attention.hpp:89-129). Pre (checked): I6, I8; base and every
-    // freq factor finite and positive; scaling's freq_scale and attn_factor
-    // finite and positive, its ext_factor and correction dims finite.
+    // S/kernels/attention.hpp:89-129). Rules: whole even heads of at most 256
+    // on a per-token x, freq_factors empty or head_dim / 2 long (I6, I8);
+    // then base, the factors, freq_scale and attn_factor finite and positive,
+    // ext_factor and the correction dims finite.
     tensor_id rope(tensor_id x, std::size_t head_dim, float base, std::span<const float> freq_factors = {},
                    rope_mode mode = rope_mode::normal, const rope_scaling& scaling = {}) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (head_dim == 0 || head_dim % 2 != 0 || head_dim > max_head_dim || size_of(x) % head_dim != 0 ||
-            !per_token(x) || (!freq_factors.empty() && freq_factors.size() != head_dim / 2)) {
-            return fail(graph_errc::bad_shape);  // I6, I8
-        }
-        const auto positive = [](float f) { return std::isfinite(f) && f > 0.0f; };
-        if (!positive(base) || !std::all_of(freq_factors.begin(), freq_factors.end(), positive) ||
-            !positive(scaling.freq_scale) || !positive(scaling.attn_factor) || !std::isfinite(scaling.ext_factor) ||
-            !std::isfinite(scaling.corr_low) || !std::isfinite(scaling.corr_high)) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, true);
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_rope{x, out, head_dim, rope_theta_scale(base, head_dim),
-                                           std::vector<float>(freq_factors.begin(), freq_factors.end()), mode,
-                                           scaling});
-        }
-        return out;
+        return emit(
+            {x},
+            [&]() -> finding {
+                const row_layout l = shape(x);
+                const bool heads_fit = head_dim != 0 && head_dim % 2 == 0 && head_dim <= max_head_dim &&
+                                       l.size % head_dim == 0;
+                const bool factors_fit = freq_factors.empty() || freq_factors.size() == head_dim / 2;
+                if (!heads_fit || !l.per_token() || !factors_fit) {
+                    return graph_errc::bad_shape;
+                }
+                const bool params_ok = positive(base) && std::all_of(freq_factors.begin(), freq_factors.end(), positive) &&
+                                       positive(scaling.freq_scale) && positive(scaling.attn_factor) &&
+                                       std::isfinite(scaling.ext_factor) && std::isfinite(scaling.corr_low) &&
+                                       std::isfinite(scaling.corr_high);
+                return params_ok ? ok : finding{graph_errc::bad_parameter};
+            },
+            [&] { return row_layout::per_run_row(shape(x).size); },
+            [&](tensor_id out) {
+                return op_rope{x, out, head_dim, rope_theta_scale(base, head_dim),
+                               std::vector<float>(freq_factors.begin(), freq_factors.end()), mode, scaling};
+            });
     }
 
     // x with each row scaled by its position's attention temperature,
     // 1 + scale * ln(floor(pos / floor_len) + 1) (S/graph/graph.hpp:678-696).
-    // Pre (checked): I8; scale finite; floor_len >= 1.
+    // Rules: per-token x (I8); then scale finite, floor_len >= 1.
     tensor_id attn_temperature(tensor_id x, float scale, std::size_t floor_len) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (!per_token(x)) {
-            return fail(graph_errc::bad_shape);  // I8
-        }
-        if (!std::isfinite(scale) || floor_len == 0) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, true);
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_attn_temperature{x, out, scale, floor_len});
-        }
-        return out;
+        return emit(
+            {x},
+            [&]() -> finding {
+                if (!shape(x).per_token()) {
+                    return graph_errc::bad_shape;
+                }
+                return std::isfinite(scale) && floor_len != 0 ? ok : finding{graph_errc::bad_parameter};
+            },
+            [&] { return row_layout::per_run_row(shape(x).size); },
+            [&](tensor_id out) { return op_attn_temperature{x, out, scale, floor_len}; });
     }
 
     // A KV cache layer of max_ctx positions (S/graph/graph.hpp:698-719).
+    // Rules: non-zero sizes, head_dim <= 256, max_ctx at most 2^32 (a 32-bit
+    // position count); then its K and V halves within the state budget (I5).
     state_id kv_cache(std::size_t max_ctx, std::size_t n_kv_heads, std::size_t head_dim) {
-        if (failed()) {
+        if (latch_.set_already()) {
             return invalid_state;
         }
-        if (max_ctx == 0 || n_kv_heads == 0 || head_dim == 0 || head_dim > max_head_dim ||
-            max_ctx > std::size_t{std::numeric_limits<std::uint32_t>::max()}) {
-            fail(graph_errc::bad_shape);
+        constexpr std::size_t positions = std::size_t{1} << 32;
+        if (max_ctx == 0 || n_kv_heads == 0 || head_dim == 0 || head_dim > max_head_dim || max_ctx > positions) {
+            reject(graph_errc::bad_shape);
             return invalid_state;
         }
-        constexpr std::size_t half = 2;
-        const std::size_t limit = max_graph_bytes - state_bytes_;
-        if (n_kv_heads > limit / head_dim || max_ctx > limit / (n_kv_heads * head_dim) / (2 * half)) {
-            fail(graph_errc::too_large);  // I5
+        // K and V, each max_ctx x n_kv_heads x head_dim binary16 values.
+        const wide bytes = wide{2} * sizeof(std::uint16_t) * max_ctx * n_kv_heads * head_dim;
+        if (bytes > max_graph_bytes - state_budget_used_) {
+            reject(graph_errc::too_large);
             return invalid_state;
         }
-        const std::size_t bytes = 2 * half * max_ctx * n_kv_heads * head_dim;
-        state_bytes_ += bytes;
-        g_.states_.push_back(state_desc{bytes, max_ctx, n_kv_heads, head_dim});
-        state_used_.push_back(false);
-        return static_cast<state_id>(g_.states_.size() - 1);
+        state_budget_used_ += static_cast<std::size_t>(bytes);
+        graph_.states_.push_back(state_desc{static_cast<std::size_t>(bytes), max_ctx, n_kv_heads, head_dim});
+        cache_taken_.push_back(0);
+        return static_cast<state_id>(graph_.states_.size() - 1);
     }
 
-    // Append (k, v) to cache at the run's positions, then attend q, as
-    // n_heads query heads, causally over the cache (S/graph/graph.hpp:727-761).
+    // Append (k, v) to the cache at the run's positions, then attend q, as
+    // n_heads query heads, causally over it (S/graph/graph.hpp:727-761).
+    // Rules: the cache exists and no other attention uses it (I7); whole heads
+    // -- q n_heads x head_dim, k and v n_kv_heads x head_dim, n_heads a
+    // multiple of n_kv_heads, an even head_dim -- on per-token tensors (I6,
+    // I8); a finite, positive scale. The scratch holds the GPU decode's
+    // split-KV partials (the reference sizes a score row per head here,
+    // S/kernels/attention.hpp:147-161).
     tensor_id attention(tensor_id q, tensor_id k, tensor_id v, state_id cache, std::size_t n_heads, float scale) {
-        if (!operand_ok(q) || !operand_ok(k) || !operand_ok(v)) {
-            return invalid_tensor;
-        }
-        if (cache >= g_.states_.size() || state_used_[cache]) {
-            return fail(graph_errc::bad_state);  // I7
-        }
-        const state_desc& c = g_.states_[cache];
-        const std::size_t row = c.n_kv_heads * c.head_dim;
-        if (n_heads == 0 || n_heads % c.n_kv_heads != 0 || n_heads > max_graph_bytes / c.head_dim ||
-            size_of(q) != n_heads * c.head_dim || size_of(k) != row || size_of(v) != row || !per_token(q) ||
-            !per_token(k) || !per_token(v) || c.head_dim % 2 != 0) {
-            return fail(graph_errc::bad_shape);  // I6, I8
-        }
-        if (!std::isfinite(scale) || scale <= 0.0f) {
-            return fail(graph_errc::bad_parameter);
-        }
-        // The GPU decode kernel's split-KV partials (the reference sizes a
-        // score row per head here, S/kernels/attention.hpp:147-161).
-        const std::size_t scratch_bytes = syn_hip_attention_scratch_bytes(
-            static_cast<uint32_t>(n_heads), static_cast<uint32_t>(c.n_kv_heads), static_cast<uint32_t>(c.head_dim),
-            static_cast<uint32_t>(c.max_ctx), static_cast<uint32_t>(g_.max_batch_));
-        const tensor_id out = add_floats(size_of(q), tensor_role::intermediate);
-        const tensor_id scratch = add_tensor(std::max<std::size_t>(scratch_bytes, 1), 0, tensor_role::scratch, false);
-        if (out == invalid_tensor || scratch == invalid_tensor) {
-            return invalid_tensor;
-        }
-        state_used_[cache] = true;
-        g_.position_limit_ = std::min(g_.position_limit_, c.max_ctx);
-        g_.nodes_.emplace_back(op_attention{q, k, v, out, scratch, cache, n_heads, scale});
-        return out;
+        return emit(
+            {q, k, v},
+            [&]() -> finding {
+                if (cache >= graph_.states_.size() || cache_taken_[cache]) {
+                    return graph_errc::bad_state;
+                }
+                const state_desc& c = graph_.states_[cache];
+                const std::size_t kv_size = c.n_kv_heads * c.head_dim;
+                const bool heads_fit = n_heads != 0 && n_heads % c.n_kv_heads == 0 &&
+                                       n_heads <= max_graph_bytes / c.head_dim && c.head_dim % 2 == 0 &&
+                                       shape(q).size == n_heads * c.head_dim && shape(k).size == kv_size &&
+                                       shape(v).size == kv_size;
+                if (!heads_fit || !shape(q).per_token() || !shape(k).per_token() || !shape(v).per_token()) {
+                    return graph_errc::bad_shape;
+                }
+                return positive(scale) ? ok : finding{graph_errc::bad_parameter};
+            },
+            [&] { return row_layout::per_run_row(shape(q).size); },
+            [&](tensor_id out, tensor_id scratch) {
+                cache_taken_[cache] = 1;
+                graph_.limits_.positions = std::min(graph_.limits_.positions, graph_.states_[cache].max_ctx);
+                return op_attention{q, k, v, out, scratch, cache, n_heads, scale};
+            },
+            [&]() -> std::optional<std::size_t> {
+                const state_desc& c = graph_.states_[cache];
+                const auto u32 = [](std::size_t x) { return static_cast<std::uint32_t>(x); };
+                return std::max<std::size_t>(
+                    syn_hip_attention_scratch_bytes(u32(n_heads), u32(c.n_kv_heads), u32(c.head_dim),
+                                                    u32(std::min<std::size_t>(c.max_ctx, 0xFFFFFFFFu)),
+                                                    u32(graph_.limits_.batch)),
+                    1);
+            });
     }
 
     // Bidirectional attention over the run's rows (S/graph/graph.hpp:831-863).
+    // Rules: q, k, v of one size, whole heads of at most 256, per-token
+    // (I6, I8); a finite, positive scale.
     tensor_id self_attention(tensor_id q, tensor_id k, tensor_id v, std::size_t n_heads, float scale) {
-        if (!operand_ok(q) || !operand_ok(k) || !operand_ok(v)) {
-            return invalid_tensor;
-        }
-        if (n_heads == 0 || size_of(q) % n_heads != 0 || size_of(k) != size_of(q) || size_of(v) != size_of(q) ||
-            !per_token(q) || !per_token(k) || !per_token(v) || size_of(q) / n_heads > max_head_dim) {
-            return fail(graph_errc::bad_shape);  // I6, I8
-        }
-        if (!std::isfinite(scale) || scale <= 0.0f) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(size_of(q), tensor_role::intermediate);
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_self_attention{q, k, v, out, n_heads, scale});
-        }
-        return out;
+        return emit(
+            {q, k, v},
+            [&]() -> finding {
+                const std::size_t size = shape(q).size;
+                const bool heads_fit = n_heads != 0 && size % n_heads == 0 && size / n_heads <= max_head_dim &&
+                                       shape(k).size == size && shape(v).size == size;
+                if (!heads_fit || !shape(q).per_token() || !shape(k).per_token() || !shape(v).per_token()) {
+                    return graph_errc::bad_shape;
+                }
+                return positive(scale) ? ok : finding{graph_errc::bad_parameter};
+            },
+            [&] { return row_layout::per_run_row(shape(q).size); },
+            [&](tensor_id out) { return op_self_attention{q, k, v, out, n_heads, scale}; });
     }
 
-    // Row n-1 of x for a run of n rows (S/graph/graph.hpp:765-781). Pre (checked): I8.
+    // Row n-1 of x for a run of n rows (S/graph/graph.hpp:765-781). Rule: per-token x (I8).
     tensor_id last_row(tensor_id x) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (!per_token(x)) {
-            return fail(graph_errc::bad_shape);  // I8
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, false);
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_last_row{x, out});
-        }
-        return out;
+        return emit(
+            {x}, [&] { return shape(x).per_token() ? ok : finding{graph_errc::bad_shape}; },
+            [&] { return row_layout::one_row(shape(x).size); },
+            [&](tensor_id out) { return op_last_row{x, out}; });
     }
 
     // (x - mean) / sqrt(var + eps) * gamma (+ beta unless empty)
-    // (S/graph/graph.hpp:783-800). Pre (checked): gamma, beta 1 x x.size;
-    // eps finite and non-negative.
+    // (S/graph/graph.hpp:783-800). Rules: gamma (and beta) 1 x size; then eps
+    // finite and non-negative, both float vectors.
     tensor_id layer_norm(tensor_id x, const matrix_ref& gamma, const matrix_ref& beta, float eps) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        const bool has_beta = !std::holds_alternative<std::monostate>(beta);
-        if (rows(gamma) != 1 || cols(gamma) != size_of(x) ||
-            (has_beta && (rows(beta) != 1 || cols(beta) != size_of(x)))) {
-            return fail(graph_errc::size_mismatch);
-        }
-        if (!std::isfinite(eps) || eps < 0.0f || !vector_ok(gamma) || (has_beta && !vector_ok(beta))) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, batched(x), row_div(x));
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_layer_norm{x, gamma, beta, eps, out});
-        }
-        return out;
-    }
-
-    tensor_id gelu(tensor_id x) {
-        return unary<op_gelu>(x);
+        return emit(
+            {x},
+            [&]() -> finding {
+                const std::size_t size = shape(x).size;
+                const bool has_beta = !std::holds_alternative<std::monostate>(beta);
+                const auto is_row = [&](const matrix_ref& m) { return rows(m) == 1 && cols(m) == size; };
+                if (!is_row(gamma) || (has_beta && !is_row(beta))) {
+                    return graph_errc::size_mismatch;
+                }
+                const bool ok_params = std::isfinite(eps) && eps >= 0.0f && float_vector(gamma) &&
+                                       (!has_beta || float_vector(beta));
+                return ok_params ? ok : finding{graph_errc::bad_parameter};
+            },
+            [&] { return shape(x); }, [&](tensor_id out) { return op_layer_norm{x, gamma, beta, eps, out}; });
     }
 
     // x with row i of table added to its row i (S/graph/graph.hpp:809-829).
-    // Pre (checked): I8; table has x.size columns and >= max_batch rows.
+    // Rules: per-token x (I8); the table x.size wide with at least max_batch
+    // rows; a float table.
     tensor_id add_rows(tensor_id x, const matrix_ref& table) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (!per_token(x)) {
-            return fail(graph_errc::bad_shape);  // I8
-        }
-        if (cols(table) != size_of(x) || rows(table) < g_.max_batch_) {
-            return fail(graph_errc::size_mismatch);
-        }
-        if (!vector_ok(table)) {
-            return fail(graph_errc::bad_parameter);
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, true);
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(op_add_rows{x, table, out});
-        }
-        return out;
+        return emit(
+            {x},
+            [&]() -> finding {
+                if (!shape(x).per_token()) {
+                    return graph_errc::bad_shape;
+                }
+                if (cols(table) != shape(x).size || rows(table) < graph_.limits_.batch) {
+                    return graph_errc::size_mismatch;
+                }
+                return float_vector(table) ? ok : finding{graph_errc::bad_parameter};
+            },
+            [&] { return row_layout::per_run_row(shape(x).size); },
+            [&](tensor_id out) { return op_add_rows{x, table, out}; });
     }
 
     // x's rows as a grid_w-wide patch grid, each s x s block of patches merged
-    // into one row of s*s*x.size floats (S/graph/graph.hpp:872-896). Pre
-    // (checked): I8, I9 (grid_w * grid_h == max_batch, both multiples of s >= 2).
+    // into one row of s*s*x.size floats (S/graph/graph.hpp:872-896). Rules:
+    // per-token x, s >= 2, a grid of max_batch patches whose sides are
+    // multiples of s (I8, I9); the merged row within the budget.
     tensor_id pixel_shuffle(tensor_id x, std::size_t grid_w, std::size_t s) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        if (!per_token(x) || s < 2 || grid_w == 0 || g_.max_batch_ % grid_w != 0 || grid_w % s != 0 ||
-            (g_.max_batch_ / grid_w) % s != 0) {
-            return fail(graph_errc::bad_shape);  // I8, I9
-        }
-        if (size_of(x) > max_graph_bytes / (s * s)) {
-            return fail(graph_errc::too_large);
-        }
-        const tensor_id out = add_floats(size_of(x) * s * s, tensor_role::intermediate, true, s * s);
-        if (out != invalid_tensor) {
-            g_.full_batch_only_ = true;
-            g_.nodes_.emplace_back(op_pixel_shuffle{x, out, grid_w, s});
-        }
-        return out;
+        return emit(
+            {x},
+            [&]() -> finding {
+                const std::size_t n = graph_.limits_.batch;
+                const bool grid_fits = s >= 2 && grid_w != 0 && n % grid_w == 0 && grid_w % s == 0 &&
+                                       (n / grid_w) % s == 0;
+                if (!shape(x).per_token() || !grid_fits) {
+                    return graph_errc::bad_shape;
+                }
+                return wide{shape(x).size} * s * s > max_graph_bytes ? finding{graph_errc::too_large} : ok;
+            },
+            [&] { return row_layout{shape(x).size * s * s, true, s * s}; },
+            [&](tensor_id out) {
+                graph_.limits_.whole_batches = true;
+                return op_pixel_shuffle{x, out, grid_w, s};
+            });
     }
 
-    // Marks t as a graph output: kept until the end of a run (I4).
+    // Marks t as a graph output, kept until the end of a run (I4). Rule: an
+    // existing, non-scratch tensor not already an output.
     void output(tensor_id t) {
-        if (failed()) {
+        if (latch_.set_already()) {
             return;
         }
-        if (t >= g_.tensors_.size() || g_.tensors_[t].role == tensor_role::scratch ||
-            g_.tensors_[t].role == tensor_role::output ||
-            std::find(g_.outputs_.begin(), g_.outputs_.end(), t) != g_.outputs_.end()) {
-            fail(graph_errc::bad_output);
+        const auto& outs = graph_.outputs_;
+        if (t >= graph_.tensors_.size() || graph_.tensors_[t].role == tensor_role::scratch ||
+            std::find(outs.begin(), outs.end(), t) != outs.end()) {
+            reject(graph_errc::bad_output);
             return;
         }
-        if (g_.tensors_[t].role == tensor_role::intermediate) {
-            g_.tensors_[t].role = tensor_role::output;
+        tensor_desc& d = graph_.tensors_[t];
+        if (d.role == tensor_role::intermediate) {
+            d.role = tensor_role::output;
         }
-        g_.outputs_.push_back(t);
+        graph_.outputs_.push_back(t);
     }
 
     result<compute_graph, graph_error> finalize() && {
-        if (error_) {
-            return graph_error{error_->first, error_->second};
+        if (latch_.set_already()) {
+            return latch_.error();
         }
-        if (g_.outputs_.empty()) {
-            return graph_error{graph_errc::no_outputs, g_.nodes_.size()};
+        if (graph_.outputs_.empty()) {
+            return graph_error{graph_errc::no_outputs, graph_.nodes_.size()};
         }
-        return std::move(g_);
+        return std::move(graph_);
     }
 
 private:
-    bool failed() const noexcept {
-        return error_.has_value();
+    using wide = unsigned __int128;
+    // A rule's finding: no error, or the code the operation fails with.
+    using finding = std::optional<graph_errc>;
+    static constexpr finding ok{};
+
+    // The first error and the node it happened at; later calls are no-ops.
+    class latch {
+    public:
+        void set(graph_errc code, std::size_t node) {
+            if (!first_) {
+                first_ = graph_error{code, node};
+            }
+        }
+        bool set_already() const noexcept {
+            return first_.has_value();
+        }
+        graph_error error() const {
+            return *first_;
+        }
+
+    private:
+        std::optional<graph_error> first_;
+    };
+
+    static bool positive(float f) noexcept {
+        return std::isfinite(f) && f > 0.0f;
+    }
+    // A matrix in a device format, whole blocks per row, with data.
+    static bool device_matrix(const matrix_ref& m) noexcept {
+        const auto* w = std::get_if<weight_view>(&m);
+        return w != nullptr && w->data != nullptr && block_values(w->type) != 0 && w->cols % block_values(w->type) == 0;
+    }
+    // A matrix the device reads as floats (biases, gammas, position tables).
+    static bool float_vector(const matrix_ref& m) noexcept {
+        return device_matrix(m) && type_of(m) == SYN_TYPE_F32;
+    }
+    // A 1 x size float vector: size_mismatch first, then bad_parameter.
+    static finding vector_rule(const matrix_ref& m, std::size_t size) noexcept {
+        if (rows(m) != 1 || cols(m) != size) {
+            return graph_errc::size_mismatch;
+        }
+        return float_vector(m) ? ok : finding{graph_errc::bad_parameter};
     }
 
-    tensor_id fail(graph_errc code) {
-        if (!error_) {
-            error_ = std::pair{code, g_.nodes_.size()};
-        }
+    tensor_id reject(graph_errc code) {
+        latch_.set(code, graph_.nodes_.size());
         return invalid_tensor;
     }
 
-    bool operand_ok(tensor_id t) {
-        if (failed()) {
+    row_layout shape(tensor_id t) const noexcept {
+        const tensor_desc& d = graph_.tensors_[t];
+        return row_layout{d.size, d.batched, d.row_div};
+    }
+
+    // Operand ids: each an existing tensor that is not a node's scratch.
+    bool usable(std::initializer_list<tensor_id> ids) {
+        if (latch_.set_already()) {
             return false;
         }
-        if (t >= g_.tensors_.size() || g_.tensors_[t].role == tensor_role::scratch) {
-            fail(graph_errc::invalid_operand);
-            return false;
+        for (const tensor_id t : ids) {
+            if (t >= graph_.tensors_.size() || graph_.tensors_[t].role == tensor_role::scratch) {
+                reject(graph_errc::invalid_operand);
+                return false;
+            }
         }
         return true;
     }
 
-    std::size_t size_of(tensor_id t) const noexcept {
-        return g_.tensors_[t].size;
+    // A tensor within the budget (I5): `bytes` (a float tensor's, or a
+    // scratch's) rounded up to plan_alignment; too_large past it.
+    tensor_id new_tensor(wide bytes, std::size_t size, tensor_role role, bool batched, std::size_t row_div) {
+        const wide rounded = (bytes + plan_alignment - 1) / plan_alignment * plan_alignment;
+        if (bytes > max_graph_bytes || rounded > max_graph_bytes - tensor_budget_used_) {
+            return reject(graph_errc::too_large);
+        }
+        tensor_budget_used_ += static_cast<std::size_t>(rounded);
+        graph_.tensors_.push_back(tensor_desc{static_cast<std::size_t>(bytes), size, role, batched, row_div});
+        return static_cast<tensor_id>(graph_.tensors_.size() - 1);
     }
-    bool batched(tensor_id t) const noexcept {
-        return g_.tensors_[t].batched;
-    }
-    std::size_t row_div(tensor_id t) const noexcept {
-        return g_.tensors_[t].row_div;
-    }
-    // Batched with one row per run row: what per-token ops take (I8).
-    bool per_token(tensor_id t) const noexcept {
-        return batched(t) && row_div(t) == 1;
-    }
-    // A matrix in a device format, whole blocks per row, with data.
-    static bool matrix_ok(const matrix_ref& m) noexcept {
-        const auto* w = std::get_if<weight_view>(&m);
-        return w != nullptr && w->data != nullptr && block_values(w->type) != 0 && w->cols % block_values(w->type) == 0;
-    }
-    // A 1 x size vector or table the device reads as floats.
-    static bool vector_ok(const matrix_ref& m) noexcept {
-        return matrix_ok(m) && type_of(m) == SYN_TYPE_F32;
+    tensor_id new_rows(const row_layout& l, tensor_role role) {
+        const std::size_t n = l.batched ? graph_.limits_.batch / l.row_div : 1;
+        return new_tensor(wide{l.size} * sizeof(float) * n, l.size, role, l.batched, l.batched ? l.row_div : 1);
     }
 
-    template <typename Op>
-    tensor_id binary(tensor_id a, tensor_id b) {
-        if (!operand_ok(a) || !operand_ok(b)) {
+    // One operation: operand ids, its rules, then its result (and scratch,
+    // when `scratch_bytes` is given; nullopt from it is too_large) and node.
+    struct no_scratch {};
+    template <class Rule, class Layout, class Make, class Scratch = no_scratch>
+    tensor_id emit(std::initializer_list<tensor_id> ids, Rule&& rule, Layout&& layout, Make&& make,
+                   Scratch&& scratch_bytes = {}) {
+        if (!usable(ids)) {
             return invalid_tensor;
         }
-        if (size_of(a) != size_of(b) || batched(a) != batched(b) || row_div(a) != row_div(b)) {
-            return fail(graph_errc::size_mismatch);  // I2, I8
+        if (const finding f = rule()) {
+            return reject(*f);
         }
-        const tensor_id out = add_floats(size_of(a), tensor_role::intermediate, batched(a), row_div(a));
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(Op{a, b, out});
+        const tensor_id out = new_rows(layout(), tensor_role::intermediate);
+        if (out == invalid_tensor) {
+            return invalid_tensor;
+        }
+        if constexpr (std::is_same_v<std::decay_t<Scratch>, no_scratch>) {
+            graph_.nodes_.emplace_back(make(out));
+        } else {
+            const std::optional<std::size_t> bytes = scratch_bytes();
+            if (!bytes) {
+                return reject(graph_errc::too_large);
+            }
+            const tensor_id scratch = new_tensor(*bytes, 0, tensor_role::scratch, false, 1);
+            if (scratch == invalid_tensor) {
+                return invalid_tensor;
+            }
+            graph_.nodes_.emplace_back(make(out, scratch));
         }
         return out;
     }
 
-    template <typename Op>
-    tensor_id unary(tensor_id x) {
-        if (!operand_ok(x)) {
-            return invalid_tensor;
-        }
-        const tensor_id out = add_floats(size_of(x), tensor_role::intermediate, batched(x), row_div(x));
-        if (out != invalid_tensor) {
-            g_.nodes_.emplace_back(Op{x, out});
-        }
-        return out;
+    // Same-layout element-wise operations (I2, I8: batching must agree).
+    template <class Make>
+    tensor_id elementwise2(tensor_id a, tensor_id b, Make&& make) {
+        return emit(
+            {a, b}, [&] { return shape(a) == shape(b) ? ok : finding{graph_errc::size_mismatch}; },
+            [&] { return shape(a); }, [&](tensor_id out) { return make(a, b, out); });
+    }
+    template <class Make>
+    tensor_id elementwise1(tensor_id x, Make&& make) {
+        return emit({x}, [] { return ok; }, [&] { return shape(x); }, [&](tensor_id out) { return make(x, out); });
     }
 
-    // A float tensor of `size` per row, max_batch / div rows if batched;
-    // the one place a float tensor's byte count is computed (checked, I5).
-    tensor_id add_floats(std::size_t size, tensor_role role, bool is_batched = true, std::size_t div = 1) {
-        const std::size_t n = is_batched ? g_.max_batch_ / div : 1;
-        if (size > max_graph_bytes / sizeof(float) / n) {
-            return fail(graph_errc::too_large);
-        }
-        const tensor_id t = add_tensor(n * size * sizeof(float), size, role, is_batched);
-        if (t != invalid_tensor) {
-            g_.tensors_[t].row_div = is_batched ? div : 1;
-        }
-        return t;
-    }
-
-    tensor_id add_tensor(std::size_t bytes, std::size_t size, tensor_role role, bool batched) {
-        const std::size_t aligned = (bytes + plan_alignment - 1) / plan_alignment * plan_alignment;
-        if (bytes > max_graph_bytes || aligned > max_graph_bytes - tensor_bytes_) {
-            return fail(graph_errc::too_large);  // I5
-        }
-        tensor_bytes_ += aligned;
-        g_.tensors_.push_back(tensor_desc{bytes, size, role, batched});
-        return static_cast<tensor_id>(g_.tensors_.size() - 1);
-    }
-
-    compute_graph g_;
-    std::vector<bool> state_used_;
-    std::size_t tensor_bytes_ = 0;
-    std::size_t state_bytes_ = 0;
-    std::optional<std::pair<graph_errc, std::size_t>> error_;
+    compute_graph graph_;
+    latch latch_;
+    std::vector<unsigned char> cache_taken_;  // per state: used by an attention node (I7)
+    std::size_t tensor_budget_used_ = 0;      // rounded tensor bytes so far (I5)
+    std::size_t state_budget_used_ = 0;       // state bytes so far (I5)
 };
 
 }  // namespace syn::graph

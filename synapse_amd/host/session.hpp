@@ -41,6 +41,11 @@ struct batch {  // tokens.size() consecutive tokens, the first at pos
 class session {
 public:
     explicit session(const compute_graph& g) : graph_(&g), plan_(plan(g)) {
+        // Run sizes go to the device as 32-bit counts.
+        if (g.max_batch() > std::numeric_limits<std::uint32_t>::max()) {
+            status_ = SYN_HIP_EUNSUPPORTED;
+            return;
+        }
         std::size_t top = plan_.arena_bytes;
         const auto& nodes = g.nodes();
         // Every bound matrix once, keyed by its host data.
@@ -72,6 +77,13 @@ public:
         }
         const std::size_t states_begin = top;
         for (const state_desc& s : g.states()) {
+            // The device KV descriptor counts positions in 32 bits; the
+            // builder accepts caches of up to 2^32 positions, as the
+            // reference's does (S/graph/graph.hpp:698-719).
+            if (s.max_ctx > std::numeric_limits<std::uint32_t>::max()) {
+                status_ = SYN_HIP_EUNSUPPORTED;
+                return;
+            }
             const auto max_ctx = static_cast<std::uint32_t>(s.max_ctx);
             const auto n_kv = static_cast<std::uint32_t>(s.n_kv_heads);
             const auto hd = static_cast<std::uint32_t>(s.head_dim);

@@ -7,7 +7,9 @@
 #include "planner.hpp"
 
 #include <cmath>
+#include <limits>
 #include <random>
+#include <vector>
 
 using namespace syn::graph;
 
@@ -52,9 +54,18 @@ void kv_cache_errors() {
         CHECK(error_of(std::move(b)) == graph_errc::bad_shape);
     }
     {
+        // a position count of at most 2^32 (S/graph/graph.hpp:703): 2^32 is
+        // accepted, one more is not
         graph_builder b;
-        CHECK(b.kv_cache(std::size_t{1} << 33, 8, 128) == invalid_state);  // not a 32-bit position
+        CHECK(b.kv_cache((std::size_t{1} << 32) + 1, 1, 2) == invalid_state);
         CHECK(error_of(std::move(b)) == graph_errc::bad_shape);
+        graph_builder ok;
+        const state_id c = ok.kv_cache(std::size_t{1} << 32, 1, 2);
+        CHECK(c == 0);
+        const tensor_id kv = ok.input(2);
+        ok.output(ok.attention(kv, kv, kv, c, 1, 0.5f));
+        auto r = std::move(ok).finalize();
+        CHECK(r.has_value() && r.value().position_limit() == (std::size_t{1} << 32));
     }
     {
         graph_builder b;
@@ -110,6 +121,238 @@ void first_error_wins() {
     CHECK(!r2.has_value() && r2.error().code == graph_errc::no_outputs);
     graph_builder zero(0);
     CHECK(error_of(std::move(zero)) == graph_errc::bad_shape);
+}
+
+// Zero-filled weights of a given format and shape, for the builder's checks
+// (it reads shapes and formats, never values).
+struct zero_weights {
+    std::vector<unsigned char> bytes;
+    weight_view view;
+    zero_weights(std::uint32_t type, std::size_t rows_, std::size_t cols_)
+        : bytes(rows_ * cols_ / block_values(type) * block_bytes(type)),
+          view{type, rows_, cols_, bytes.data()} {}
+    matrix_ref ref() const { return matrix_ref{view}; }
+};
+
+// The reference's builder cases (tests/sdk/graph_builder.cpp:21-284), restated
+// for this builder: the same graphs, the same codes at the same nodes.
+// Scratch sizes are this build's (the GPU kernels' buffers).
+void reference_builder_cases() {
+    // builds a valid graph in topological order (:21-58)
+    {
+        const zero_weights w(SYN_TYPE_Q4_K, 512, 256), gamma(SYN_TYPE_F32, 1, 256);
+        graph_builder b;
+        const tensor_id x = b.input(256);
+        const tensor_id h = b.rms_norm(x, gamma.ref(), 1e-5f);
+        const tensor_id y = b.matmul(w.ref(), h);
+        const tensor_id z = b.silu(y);
+        b.output(z);
+        auto r = std::move(b).finalize();
+        CHECK(r.has_value());
+        const compute_graph& g = r.value();
+        CHECK(g.inputs().size() == 1 && g.outputs().size() == 1 && g.nodes().size() == 3);
+        CHECK(g.tensors()[y].size == 512 && g.tensors()[z].role == tensor_role::output);
+        const auto& mm = std::get<op_matmul>(g.nodes()[1]);
+        CHECK(g.tensors()[mm.scratch].role == tensor_role::scratch);
+        CHECK(g.tensors()[mm.scratch].bytes == syn_hip_matmul_q_act_bytes(SYN_TYPE_Q4_K, 1, 256));
+        for (std::size_t i = 0; i < g.nodes().size(); ++i) {  // I1
+            for (tensor_id t : operands(g.nodes()[i])) {
+                bool earlier = g.tensors()[t].role == tensor_role::input;
+                for (std::size_t j = 0; j < i; ++j) {
+                    for (tensor_id res : results(g.nodes()[j])) {
+                        earlier = earlier || res == t;
+                    }
+                }
+                CHECK(earlier);
+            }
+        }
+    }
+    // rejects mismatched sizes and reports the node (:60-73)
+    {
+        const zero_weights w(SYN_TYPE_Q8_0, 64, 128);
+        graph_builder b;
+        const tensor_id y = b.silu(b.input(256));
+        CHECK(b.matmul(w.ref(), y) == invalid_tensor);
+        b.output(y);
+        auto r = std::move(b).finalize();
+        CHECK(!r.has_value() && r.error().code == graph_errc::size_mismatch && r.error().node == 1);
+    }
+    // the first error wins and later calls are no-ops (:75-85)
+    {
+        graph_builder b;
+        const tensor_id a = b.input(8), c = b.input(16);
+        CHECK(b.add(a, c) == invalid_tensor);
+        CHECK(b.silu(a) == invalid_tensor);
+        CHECK(b.input(4) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::size_mismatch);
+    }
+    // invalid operands, empty inputs, bad outputs (:87-128)
+    {
+        graph_builder b;
+        CHECK(b.silu(42) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::invalid_operand);
+    }
+    {
+        graph_builder b;
+        CHECK(b.input(0) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::empty_tensor);
+    }
+    {
+        graph_builder b;
+        b.input(8);
+        CHECK(error_of(std::move(b)) == graph_errc::no_outputs);
+    }
+    {
+        graph_builder b;
+        const tensor_id y = b.silu(b.input(8));
+        b.output(y);
+        b.output(y);
+        CHECK(error_of(std::move(b)) == graph_errc::bad_output);
+    }
+    {
+        const zero_weights w(SYN_TYPE_Q8_0, 32, 32);
+        graph_builder b;
+        const tensor_id y = b.matmul(w.ref(), b.input(32));
+        b.output(y + 1);  // the matmul's scratch tensor
+        CHECK(error_of(std::move(b)) == graph_errc::bad_output);
+    }
+    {
+        const zero_weights gamma(SYN_TYPE_F32, 2, 8);  // not a row vector
+        graph_builder b;
+        CHECK(b.rms_norm(b.input(8), gamma.ref(), 1e-5f) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::size_mismatch);
+    }
+    // sizes whose byte counts would overflow (:130-156)
+    {
+        graph_builder b;
+        CHECK(b.input(std::numeric_limits<std::size_t>::max() / 2) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::too_large);
+    }
+    {
+        graph_builder b;
+        const std::size_t quarter = (max_graph_bytes / 4 - plan_alignment) / sizeof(float);
+        for (int i = 0; i < 4; ++i) {
+            CHECK(b.input(quarter) != invalid_tensor);
+        }
+        CHECK(b.input(quarter) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::too_large);
+    }
+    {
+        graph_builder b;
+        const tensor_id x = b.input(max_graph_bytes / sizeof(float) / 2);
+        CHECK(x != invalid_tensor);
+        CHECK(b.silu(x) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::too_large);
+    }
+    // embed, rope, and attention over a KV cache (:158-185)
+    {
+        const zero_weights table(SYN_TYPE_Q8_0, 100, 64);
+        graph_builder b;
+        const tensor_id x = b.embed(table.ref());
+        const tensor_id q = b.rope(x, 16, 10000.0f);
+        const tensor_id k = b.rope(b.silu(x), 16, 10000.0f);
+        const tensor_id v = b.silu(x);
+        const state_id small = b.kv_cache(32, 4, 16);
+        const state_id large = b.kv_cache(64, 4, 16);
+        const tensor_id a = b.attention(q, k, v, small, 4, 0.25f);
+        const tensor_id a2 = b.attention(q, k, v, large, 4, 0.25f);
+        b.output(b.add(a, a2));
+        auto r = std::move(b).finalize();
+        CHECK(r.has_value());
+        const compute_graph& g = r.value();
+        CHECK(g.inputs().empty() && g.token_limit() == 100 && g.position_limit() == 32);
+        CHECK(g.states().size() == 2 && g.states()[small].bytes == 2 * 32 * 4 * 16 * sizeof(std::uint16_t));
+        const auto& op = std::get<op_attention>(g.nodes()[5]);
+        CHECK((operands(g.nodes()[5]) == std::vector<tensor_id>{q, k, v}));
+        CHECK((results(g.nodes()[5]) == std::vector<tensor_id>{a, op.scratch}));
+        CHECK(g.tensors()[op.scratch].role == tensor_role::scratch);
+        CHECK(g.tensors()[op.scratch].bytes == std::max<std::uint64_t>(syn_hip_attention_scratch_bytes(4, 4, 16, 32, 1), 1));
+    }
+    // head layouts and parameters that do not fit (:187-234)
+    const auto code = [](auto build) {
+        graph_builder b;
+        build(b);
+        return error_of(std::move(b));
+    };
+    CHECK(code([](graph_builder& b) { b.rope(b.input(30), 15, 1e4f); }) == graph_errc::bad_shape);
+    CHECK(code([](graph_builder& b) { b.rope(b.input(30), 4, 1e4f); }) == graph_errc::bad_shape);
+    CHECK(code([](graph_builder& b) {
+              const float f[3] = {1, 1, 1};
+              b.rope(b.input(32), 8, 1e4f, f);
+          }) == graph_errc::bad_shape);
+    CHECK(code([](graph_builder& b) { b.rope(b.input(32), 8, std::nanf("")); }) == graph_errc::bad_parameter);
+    CHECK(code([](graph_builder& b) {
+              const float f[4] = {1, 0, 1, 1};
+              b.rope(b.input(32), 8, 1e4f, f);
+          }) == graph_errc::bad_parameter);
+    CHECK(code([](graph_builder& b) { b.kv_cache(0, 2, 8); }) == graph_errc::bad_shape);
+    CHECK(code([](graph_builder& b) { b.kv_cache(8, 2, max_head_dim + 2); }) == graph_errc::bad_shape);
+    CHECK(code([](graph_builder& b) { b.kv_cache(std::size_t{1} << 30, std::size_t{1} << 28, 64); }) ==
+          graph_errc::too_large);
+    const auto attend = [](std::size_t q_size, std::size_t n_heads, float scale) {
+        return [=](graph_builder& b) {
+            const tensor_id q = b.input(q_size);
+            const tensor_id kv = b.input(16);  // 2 KV heads of 8
+            b.attention(q, kv, kv, b.kv_cache(8, 2, 8), n_heads, scale);
+        };
+    };
+    CHECK(code(attend(24, 3, 1.0f)) == graph_errc::bad_shape);
+    CHECK(code(attend(24, 4, 1.0f)) == graph_errc::bad_shape);
+    CHECK(code(attend(32, 4, 0.0f)) == graph_errc::bad_parameter);
+    CHECK(code([](graph_builder& b) {
+              const tensor_id t = b.input(16);
+              b.attention(t, t, t, 0, 2, 1.0f);
+          }) == graph_errc::bad_state);
+    CHECK(code([](graph_builder& b) {
+              const tensor_id t = b.input(16);
+              const state_id c = b.kv_cache(8, 2, 8);
+              b.attention(t, t, t, c, 2, 1.0f);
+              b.attention(t, t, t, c, 2, 1.0f);
+          }) == graph_errc::bad_state);
+    CHECK(code([](graph_builder& b) { b.embed(matrix_ref{}); }) == graph_errc::empty_tensor);
+    // batched graphs size tensors for max_batch rows (:236-255)
+    {
+        const zero_weights w(SYN_TYPE_Q8_0, 64, 32);
+        graph_builder b(8);
+        const tensor_id x = b.input(32);
+        const tensor_id y = b.matmul(w.ref(), x);
+        const tensor_id last = b.last_row(y);
+        const tensor_id z = b.silu(last);
+        b.output(z);
+        auto r = std::move(b).finalize();
+        CHECK(r.has_value());
+        const compute_graph& g = r.value();
+        CHECK(g.max_batch() == 8 && g.rows(x) == 8 && g.tensors()[x].bytes == 8 * 32 * sizeof(float));
+        CHECK(g.rows(y) == 8 && g.rows(last) == 1 && g.rows(z) == 1);
+        const auto& mm = std::get<op_matmul>(g.nodes()[0]);
+        CHECK(g.tensors()[mm.scratch].bytes == syn_hip_matmul_q_act_bytes(SYN_TYPE_Q8_0, 8, 32));
+    }
+    // ops that mix batched and single-row tensors (I8) (:257-284)
+    const auto code4 = [](auto build) {
+        graph_builder b(4);
+        build(b);
+        return error_of(std::move(b));
+    };
+    CHECK(code4([](graph_builder& b) {
+              const tensor_id x = b.input(16);
+              b.add(x, b.last_row(x));
+          }) == graph_errc::size_mismatch);
+    CHECK(code4([](graph_builder& b) { b.rope(b.last_row(b.input(16)), 8, 1e4f); }) == graph_errc::bad_shape);
+    CHECK(code4([](graph_builder& b) { b.last_row(b.last_row(b.input(16))); }) == graph_errc::bad_shape);
+    CHECK(code4([](graph_builder& b) {
+              const tensor_id x = b.input(16);
+              b.attention(b.last_row(x), x, x, b.kv_cache(8, 2, 8), 2, 1.0f);
+          }) == graph_errc::bad_shape);
+    {
+        graph_builder b(0);
+        CHECK(b.input(4) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::bad_shape);
+    }
+    {
+        graph_builder b(std::numeric_limits<std::size_t>::max() / 8);  // max_batch * size * 4 wraps
+        CHECK(b.input(64) == invalid_tensor);
+        CHECK(error_of(std::move(b)) == graph_errc::too_large);
+    }
 }
 
 void self_attention_errors() {
@@ -298,6 +541,7 @@ void model_op_errors() {
 }  // namespace
 
 int main() {
+    reference_builder_cases();
     model_op_errors();
     llama_attention_wiring();
     kv_cache_errors();

@@ -75,6 +75,12 @@ def test_graph_builder_and_planner():
     _run("test_graph")
 
 
+def test_session_run_allocates_nothing():
+    """session::run under a counting operator new, against a C ABI that
+    launches nothing (tests/sdk/graph_no_alloc.cpp:199-263 restated)."""
+    _run("test_no_alloc")
+
+
 @pytest.mark.gpu
 def test_session_against_the_oracle():
     _run("test_session")

@@ -40,9 +40,9 @@ def _vision(arena, n, batch, n_heads, hd, dtype, sigma=0.5, seed=3, images=None)
 
 def test_vision_clip_vit_l14(arena):
     """Config 5 at full size: 32 images x 257 rows, 16 heads of 64, f16
-    inputs ~ N(0, 0.5^2); four images checked against the oracle."""
+    inputs ~ N(0, 0.5^2); every image checked against the oracle."""
     c = wl.C5
-    _vision(arena, c.n, c.batch, c.n_heads, c.head_dim, SYN_F16, c.sigma, seed=wl.SEED, images=[0, 7, 20, 31])
+    _vision(arena, c.n, c.batch, c.n_heads, c.head_dim, SYN_F16, c.sigma, seed=wl.SEED)
 
 
 @pytest.mark.parametrize("n,hd", [(37, 8), (1, 8), (6, 16), (50, 24), (130, 64), (257, 128), (64, 256),

@@ -129,6 +129,41 @@ def test_q_is_rounded_to_binary16_before_the_dot():
     assert np.array_equal(outs[0], outs[1])
 
 
+def test_normalised_probabilities_are_rounded_to_binary16():
+    """attend_group rounds each normalised p to binary16 before p.V
+    (S/kernels/attention.hpp:222-227). With one-hot V rows (V_t = e_t, t <
+    hd) output element d is p_d times exactly 1, so every output element is
+    a binary16 value, and element d equals the binary16 rounding of the
+    double-precision softmax weight of position d to within one binary16
+    step. Dropping that rounding leaves float weights, which are almost never
+    binary16 values: the first assertion then fails."""
+    n_heads, n_kv, hd, pos = 4, 2, 64, 39  # 40 positions attended
+    g = _rng(7)
+    n = pos + 1
+    q = (g.standard_normal((n, n_heads * hd)) * 2).astype(np.float32)
+    k = (g.standard_normal((n, n_kv * hd)) * 2).astype(np.float32)
+    v = np.zeros((n, n_kv * hd), np.float32)
+    for t in range(n):
+        for kv in range(n_kv):
+            v[t, kv * hd + t] = 1.0
+    kc, vc = orc.new_cache(n, n_kv, hd)
+    scale = 0.125
+    out = orc.attention_rows(q, k, v, 0, kc, vc, n_heads, scale)[pos]  # the last token sees all 40 rows
+    assert np.array_equal(out.astype(np.float16).astype(np.float32), out)
+    group = n_heads // n_kv
+    for h in range(n_heads):
+        kv = h // group
+        qh = q[pos, h * hd:(h + 1) * hd].astype(np.float16).astype(np.float64)
+        kh = k[:, kv * hd:(kv + 1) * hd].astype(np.float16).astype(np.float64)
+        s_ = kh @ qh * scale
+        p_ = np.exp(s_ - s_.max())
+        p_ /= p_.sum()
+        got = out[h * hd:h * hd + n].astype(np.float64)
+        step = np.abs(np.spacing(p_.astype(np.float16)).astype(np.float64))
+        assert np.all(np.abs(got - p_) <= step), h
+        assert np.all(out[h * hd + n:(h + 1) * hd] == 0.0)
+
+
 def test_causal_horizon():
     """Changing rows after position p leaves tokens up to p unchanged, and
     changes token p + 1."""

@@ -319,30 +319,113 @@ def bench_gemm(hip: Hip, reps: int, n: int = 512):
     return out
 
 
+# The box gives one GPU a share of 16 host CPUs, whatever os.cpu_count() says.
+HOST_THREAD_SHARE = 16
+
+
+def _oracle():
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import binding as orc
+    return orc
+
+
+def _best_of(fn, budget_s: float, min_runs: int = 3):
+    """Runs fn until budget_s has passed and at least min_runs times; the
+    fastest run in seconds and the run count."""
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < min_runs:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return min(times), len(times)
+
+
+def _host_threads(cap: int) -> int:
+    return max(1, min(cap, HOST_THREAD_SHARE, len(os.sched_getaffinity(0))))
+
+
 def cpu_baseline(cfg: wl.Decode, budget_s: float):
     """The CPU oracle (oracle/liboracle.so, a port of the reference's
     attention()) timed on this host: full config-2 decode steps, threads over
-    the 8 KV groups as the reference's session splits them."""
-    sys.path.insert(0, str(ROOT / "oracle"))
-    import binding as orc
-
+    the 8 KV groups as the reference's session splits them
+    (S/graph/session.hpp:360)."""
+    orc = _oracle()
     kc, vc, q, k, v = wl.decode_inputs(cfg)
     ok_k, ok_v = orc.new_cache(cfg.ctx + 1, cfg.n_kv, cfg.head_dim)
     ok_k[: cfg.ctx], ok_v[: cfg.ctx] = kc, vc
-    threads = min(cfg.n_kv, len(os.sched_getaffinity(0)))
+    threads = _host_threads(cfg.n_kv)
     scores = np.zeros(orc.scratch_floats(cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.ctx + 1), np.float32)
-    times = []
-    t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or len(times) < 3:
-        t = time.perf_counter()
-        orc.attend_rows(q, cfg.ctx, ok_k, ok_v, cfg.n_heads, cfg.scale, threads=threads, scores=scores)
-        times.append(time.perf_counter() - t)
-    best = min(times)
+    best, runs = _best_of(lambda: orc.attend_rows(q, cfg.ctx, ok_k, ok_v, cfg.n_heads, cfg.scale, threads=threads,
+                                                  scores=scores), budget_s)
     return {"value": round(cfg.kv_bytes() / best / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} config-2 decode steps (attend over 4097 cached rows, 32 heads), best of "
-                      f"{len(times)}; oracle/liboracle.so, {threads} threads over KV groups, "
+            "sample": f"{runs} config-2 decode steps (attend over 4097 cached rows, 32 heads), best of "
+                      f"{runs}; oracle/liboracle.so, {threads} threads over KV groups, "
                       f"{os.cpu_count()} host CPUs visible",
             "ms_per_step": round(best * 1e3, 3)}
+
+
+def cpu_prefill(cfg: wl.Prefill, budget_s: float):
+    """Config 3 on the CPU oracle: the whole op (append 2048 rows, causal
+    attention), threads over the KV groups (S/graph/session.hpp:360)."""
+    orc = _oracle()
+    q, k, v = wl.prefill_inputs(cfg)
+    kc, vc = orc.new_cache(cfg.n, cfg.n_kv, cfg.head_dim)
+    threads = _host_threads(cfg.n_kv)
+    best, runs = _best_of(lambda: orc.attention_rows(q, k, v, 0, kc, vc, cfg.n_heads, cfg.scale, threads=threads),
+                          budget_s)
+    return {"tflops": round(cfg.flops() / best / 1e12, 4), "ms": round(best * 1e3, 2),
+            "tokens_per_s": round(cfg.n / best, 1), "cores": threads, "kind": "port",
+            "sample": f"whole config-3 op (append + attend, 2048 rows), best of {runs}; {threads} threads over "
+                      f"KV groups"}
+
+
+def cpu_ragged(cfg: wl.Ragged, budget_s: float):
+    """Config 4 on the CPU oracle: each of the 16 sequences attends its own
+    cache in turn, threads over its KV groups (S/graph/session.hpp:360). The
+    inputs are bench_ragged's (same seed, K and V share one array)."""
+    orc = _oracle()
+    lengths = [int(x) for x in cfg.lengths()]
+    row = cfg.n_kv * cfg.head_dim
+    qsz = cfg.n_heads * cfg.head_dim
+    g = wl.rng(wl.SEED + 9)
+    seqs = []
+    for L in lengths:
+        kc = wl.to_f16_bits(wl.normal(g, (L, row)))
+        seqs.append((kc, wl.normal(g, (1, qsz)), L))
+    threads = _host_threads(cfg.n_kv)
+    scores = np.zeros(orc.scratch_floats(cfg.n_heads, cfg.n_kv, cfg.head_dim, max(lengths)), np.float32)
+
+    def batch():
+        for kc, q, L in seqs:
+            orc.attend_rows(q, L - 1, kc, kc, cfg.n_heads, cfg.scale, threads=threads, scores=scores)
+
+    best, runs = _best_of(batch, budget_s)
+    nbytes = sum(L * row * 2 * 2 for L in lengths) + cfg.n_seqs * qsz * 8
+    return {"gbs": round(nbytes / best / 1e9, 3), "ms": round(best * 1e3, 2),
+            "seqs_per_s": round(cfg.n_seqs / best, 1), "cores": threads, "kind": "port",
+            "sample": f"all 16 sequences ({sum(lengths)} cached rows), best of {runs}; {threads} threads over "
+                      f"KV groups"}
+
+
+def cpu_vision(cfg: wl.Vision, budget_s: float):
+    """Config 5 on the CPU oracle: the 32 images one after another, each
+    split into head x 16 query blocks over the threads
+    (S/graph/session.hpp:419-448)."""
+    orc = _oracle()
+    q, k, v = wl.vision_inputs(cfg)
+    threads = _host_threads(cfg.n_heads * 16)
+    n = cfg.n
+
+    def batch():
+        for b in range(cfg.batch):
+            sl = slice(b * n, (b + 1) * n)
+            orc.self_attention(q[sl], k[sl], v[sl], cfg.n_heads, cfg.scale, threads=threads)
+
+    best, runs = _best_of(batch, budget_s)
+    return {"tflops": round(cfg.flops() / best / 1e12, 4), "ms": round(best * 1e3, 2),
+            "images_per_s": round(cfg.batch / best, 1), "cores": threads, "kind": "port",
+            "sample": f"all 32 images, best of {runs}; {threads} threads over head x 16 query blocks"}
 
 
 def main() -> int:
@@ -438,6 +521,12 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+        side = args.cpu_seconds / 4
+        for key, fn, c in (("prefill", cpu_prefill, wl.C3), ("ragged", cpu_ragged, wl.C4),
+                           ("vision", cpu_vision, wl.C5)):
+            if key in extra:
+                extra[key]["cpu"] = fn(c, side)
+                log(f"cpu {key}: {extra[key]['cpu']}")
     print(json.dumps(line), flush=True)
     return 0
 

@@ -767,6 +767,10 @@ int syn_hip_self_attention(syn_arena* a, const syn_self_desc* d) {
     f.q_row = static_cast<uint32_t>(size);
     f.row = static_cast<uint32_t>(size);
     f.scale_log2e = d->scale * syn::log2e;
+    f.scale = d->scale;
+    if (d->in_dtype == SYN_F32 && syn::self_f32_fits(d->n)) {
+        return hip_status(syn::launch_self_f32(f, a->stream), "self_attention launch");
+    }
     if (fast_shape(d->head_dim)) {
         return hip_status(syn::launch_bidirectional(f, d->in_dtype, a->stream), "self_attention launch");
     }

@@ -81,14 +81,14 @@ struct decode_traits;
 template <>
 struct decode_traits<decode_one_args> {
     static constexpr bool multi = false;
-    __device__ static const decode_seq& seq(const decode_one_args& a, uint32_t) { return a.s; }
+    __host__ __device__ static const decode_seq& seq(const decode_one_args& a, uint32_t) { return a.s; }
     __device__ static uint32_t find(const decode_one_args&, uint32_t) { return 0; }
     __device__ static uint32_t find_merge(const decode_one_args&, uint32_t) { return 0; }
 };
 template <>
 struct decode_traits<decode_batch_args> {
     static constexpr bool multi = true;
-    __device__ static const decode_seq& seq(const decode_batch_args& a, uint32_t i) { return a.seq[i]; }
+    __host__ __device__ static const decode_seq& seq(const decode_batch_args& a, uint32_t i) { return a.seq[i]; }
     __device__ static uint32_t find(const decode_batch_args& a, uint32_t sb) {
         return find_seq(a.block0s, a.p.n_seqs, sb);
     }
@@ -117,7 +117,10 @@ constexpr int vmcnt_imm(int n) {
     return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
-template <int HDP, bool QF16, class A>
+// SHORT: some sequence of the launch has at most decode_chunk_unit rows and
+// takes the whole-softmax path below; launches without one compile it out
+// (it costs the online path about 60 registers).
+template <int HDP, bool QF16, bool SHORT, class A>
 __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     using T = decode_traits<A>;
     constexpr bool MULTI = T::multi;
@@ -271,8 +274,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         }
     };
 
-    // One 32-position step of the wave on loaded K, V.
-    const auto step = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
+    // The parts of one 32-position step of the wave on loaded K, V.
+    // inject_new: kv_append (S/kernels/attention.hpp:165-175) of the step's
+    // new row, from its LDS copy, into this step's operands and the cache.
+    const auto inject_new = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
         const uint32_t tv = tb + 8 * G;
         if (new_here && tb + decode_positions_per_wave > new_t) {
             // kv_append (S/kernels/attention.hpp:165-175) of the new row, from
@@ -321,8 +326,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
                 }
             }
         }
-
-        f4 sc[2];
+    };
+    // scores: raw q.k of head r at positions tv + 4e + i in sc[e][i], -inf
+    // past the split end; returns their max over the wave's 32 positions.
+    const auto scores = [&](uint32_t tv, u4 (&kr)[2][NS], f4 (&sc)[2]) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             sc[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -342,28 +349,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
                 bm = fmaxf(bm, sc[e][i]);
             }
         }
-        bm = max32(max16(bm));
-        const float m_new = fmaxf(m_run, bm);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = fast_exp2((m_run - m_use) * c);
-        h8 pa;
-        float ps = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const _Float16 ph = to_h(fast_exp2((sc[e][i] - m_use) * c));
-                pa[4 * e + i] = ph;
-                ps += static_cast<float>(ph);
-            }
-        }
-        l_run = l_run * alpha + sum32(sum16(ps));
-        m_run = m_new;
-        // The O^T accumulator's column is this lane's head: rescale by its own alpha.
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            o[n] *= alpha;
-        }
+        return max32(max16(bm));
+    };
+    // accumulate: O^T += V^T . P^T for the step's probabilities pa.
+    const auto accumulate = [&](uint32_t tv, u4 (&vr)[NT], h8 pa) {
         // Positions past the split end carry p = 0; zero their V too, so a
         // stale non-finite half past the cache's length cannot reach O.
         if (tv + 8 > t_end) {
@@ -387,6 +376,37 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         }
     };
 
+    // One online-softmax step: p = exp(s - running max) rounded to f16, the
+    // running sum and O rescaled when the max grows.
+    const auto step = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
+        const uint32_t tv = tb + 8 * G;
+        inject_new(tb, kr, vr);
+        f4 sc[2];
+        const float bm = scores(tv, kr, sc);
+        const float m_new = fmaxf(m_run, bm);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = fast_exp2((m_run - m_use) * c);
+        h8 pa;
+        float ps = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 ph = to_h(fast_exp2((sc[e][i] - m_use) * c));
+                pa[4 * e + i] = ph;
+                ps += static_cast<float>(ph);
+            }
+        }
+        l_run = l_run * alpha + sum32(sum16(ps));
+        m_run = m_new;
+        // The O^T accumulator's column is this lane's head: rescale by its own alpha.
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            o[n] *= alpha;
+        }
+        accumulate(tv, vr, pa);
+    };
+
     // The wave's first K, V loads go out with q's; later steps load their
     // 32 positions at the top of the step.
     constexpr uint32_t stride = decode_positions_per_wave * decode_waves;
@@ -396,11 +416,73 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         load_kv(tb, kr, vr);
     }
     convert_q(tb < t_end);
-    while (tb < t_end) {
-        step(tb, kr, vr);
-        tb += stride;
-        if (tb < t_end) {
-            load_kv(tb, kr, vr);
+    float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));
+    // A sequence of at most 128 rows is one split in which every wave takes
+    // at most one step. Its softmax is then taken whole, as attend_group
+    // takes it (S/kernels/attention.hpp:222-227): max and sum over all the
+    // sequence's positions first (exchanged through LDS), then
+    // p = exp(s - max) * (1 / sum) rounded to binary16, so the rounding falls
+    // on the normalised probability, as the reference's does, and O needs no
+    // final division. Longer sequences round the unnormalised p of the
+    // online softmax and divide at the end.
+    const bool whole = SHORT && s.len <= decode_chunk_unit;
+    if (whole) {
+        const bool have = tb < t_end;  // wave-uniform
+        const uint32_t tv = tb + 8 * G;
+        f4 sc[2];
+        float bm = -INFINITY;
+        if (have) {
+            inject_new(tb, kr, vr);
+            bm = scores(tv, kr, sc);
+        } else {
+            sc[0] = sc[1] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        }
+        if (G == 0) {
+            lds_ml[(w * 16 + r) * 2] = bm;
+        }
+        lds_barrier();
+        float mx = lds_ml[r * 2];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) {
+            mx = fmaxf(mx, lds_ml[(v * 16 + r) * 2]);
+        }
+        const float m_use = mx == -INFINITY ? 0.0f : mx;
+        float ex[8];
+        float es = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ex[4 * e + i] = fast_exp2((sc[e][i] - m_use) * c);  // 0 past the end
+                es += ex[4 * e + i];
+            }
+        }
+        es = sum32(sum16(es));
+        if (G == 0) {
+            lds_ml[(w * 16 + r) * 2 + 1] = es;
+        }
+        lds_barrier();
+        float total = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            total += lds_ml[(v * 16 + r) * 2 + 1];
+        }
+        const float inv = 1.0f / total;
+        h8 pa;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            pa[j] = to_h(ex[j] * inv);
+        }
+        if (have) {
+            accumulate(tv, vr, pa);
+        }
+    } else {
+        while (tb < t_end) {
+            step(tb, kr, vr);
+            tb += stride;
+            if (tb < t_end) {
+                load_kv(tb, kr, vr);
+            }
         }
     }
 
@@ -408,11 +490,12 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // Each wave leaves its per-head (max, sum) and its unscaled O^T in its own
     // LDS slot (head rows padded by 4 floats against bank conflicts); then
     // every thread combines the 4 slots for its output elements. Lane (G, r)
-    // holds O^T[16n + 4G + i][head r] in o[n][i].
+    // holds O^T[16n + 4G + i][head r] in o[n][i]. A whole-softmax sequence's
+    // waves hold normalised parts of one sum (and other waves may still be
+    // reading the (max, sum) slots), so they write O only.
     const uint32_t orow = hd + 4;
-    float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));
     float* lds_o = lds_ml + 4 * 16 * 2;
-    if (G == 0) {
+    if (G == 0 && !whole) {
         lds_ml[(w * 16 + r) * 2] = m_run;
         lds_ml[(w * 16 + r) * 2 + 1] = l_run;
     }
@@ -438,6 +521,15 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     for (uint32_t e = 4 * tid; e < nout; e += 4 * 256) {
         const uint32_t h = e / hd;
         const uint32_t d = e % hd;
+        if (whole) {
+            f4 acc = *reinterpret_cast<const f4*>(lds_o + h * orow + d);
+#pragma unroll
+            for (int v = 1; v < 4; ++v) {
+                acc += *reinterpret_cast<const f4*>(lds_o + (v * group + h) * orow + d);
+            }
+            *reinterpret_cast<f4*>(s.out + static_cast<std::size_t>(h0) * hd + e) = acc;
+            continue;
+        }
         float mw[4];
         float mx = -INFINITY;
 #pragma unroll
@@ -590,11 +682,13 @@ template <int HDP, class A>
 hipError_t launch_hdp(const A& a, uint32_t q_dtype, hipStream_t stream) {
     const std::size_t lds = decode_lds_bytes(a.p.group, a.p.hd);
     const dim3 grid(a.p.total_slots);
-    if (q_dtype == 1) {
-        decode_kernel<HDP, true, A><<<grid, 256, lds, stream>>>(a);
-    } else {
-        decode_kernel<HDP, false, A><<<grid, 256, lds, stream>>>(a);
+    bool any_short = false;
+    for (uint32_t i = 0; i < a.p.n_seqs; ++i) {
+        any_short = any_short || decode_traits<A>::seq(a, i).len <= decode_chunk_unit;
     }
+    const auto kernel = q_dtype == 1 ? (any_short ? decode_kernel<HDP, true, true, A> : decode_kernel<HDP, true, false, A>)
+                                     : (any_short ? decode_kernel<HDP, false, true, A> : decode_kernel<HDP, false, false, A>);
+    kernel<<<grid, 256, lds, stream>>>(a);
     if (a.p.merge_blocks > 0) {
         decode_merge_kernel<A><<<a.p.merge_blocks, 256, 0, stream>>>(a);
     }

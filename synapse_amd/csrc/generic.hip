@@ -83,7 +83,80 @@ __global__ __launch_bounds__(64) void generic_kernel(const flash_args a) {
     }
 }
 
+// Image-encoder attention on f32 rows with the reference's arithmetic
+// (self_attend_head, S/kernels/attention.hpp:324-486): a score is
+// acc = fma(q_d, k_d, acc) over d from 0, times scale; softmax over the
+// image's keys in f32 with the max subtracted, a double sum and a multiply by
+// float(1 / sum) (S/kernels/elementwise.hpp:174-201); an output element is
+// acc = fma(p_j, v_j, acc) over j from 0. No binary16 anywhere, so f32 inputs
+// keep f32 precision end to end. One wave per (query row, head, image): lane
+// l scores keys l, l + 64, ... (each chain in order), the probabilities sit
+// in LDS, and lane l then sums output dims l, l + 64, ... over the keys in
+// order. The f16-input and long-image shapes take the matrix-core kernel.
+__global__ __launch_bounds__(64) void self_f32_kernel(const flash_args a) {
+    extern __shared__ float probs[];  // n
+    const int ln = threadIdx.x;
+    const uint32_t i = blockIdx.x;
+    const uint32_t h = blockIdx.y;
+    const uint32_t img = blockIdx.z;
+    const uint32_t hd = a.hd;
+    const uint32_t n = a.n;
+    const std::size_t row_base = static_cast<std::size_t>(img) * n;
+    const float* q = static_cast<const float*>(a.q) + (row_base + i) * a.q_row + static_cast<std::size_t>(h) * hd;
+    const float* kb = static_cast<const float*>(a.k_rows) + row_base * a.row + static_cast<std::size_t>(h) * hd;
+    const float* vb = static_cast<const float*>(a.v_rows) + row_base * a.row + static_cast<std::size_t>(h) * hd;
+
+    float mx = -INFINITY;
+    for (uint32_t j = ln; j < n; j += 64) {
+        const float* kj = kb + static_cast<std::size_t>(j) * a.row;
+        float acc = 0.0f;
+        for (uint32_t d = 0; d < hd; ++d) {
+            acc = fmaf(q[d], kj[d], acc);
+        }
+        const float sj = acc * a.scale;
+        probs[j] = sj;
+        mx = fmaxf(mx, sj);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        mx = xor_max(mx, m);
+    }
+    double sum = 0.0;
+    for (uint32_t j = ln; j < n; j += 64) {
+        const float e = expf(probs[j] - mx);
+        probs[j] = e;
+        sum += e;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        sum += __shfl_xor(sum, m, wave);
+    }
+    const auto inv = static_cast<float>(1.0 / sum);
+    for (uint32_t j = ln; j < n; j += 64) {
+        probs[j] *= inv;
+    }
+    __syncthreads();  // every lane reads every probability below
+    float* out = a.out + (row_base + i) * a.q_row + static_cast<std::size_t>(h) * hd;
+    for (uint32_t e = ln; e < hd; e += 64) {
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < n; ++j) {
+            acc = fmaf(probs[j], vb[static_cast<std::size_t>(j) * a.row + e], acc);
+        }
+        out[e] = acc;
+    }
+}
+
 }  // namespace
+
+bool self_f32_fits(uint32_t n) {
+    return n <= self_f32_max_keys;
+}
+
+hipError_t launch_self_f32(const flash_args& a, hipStream_t stream) {
+    const dim3 grid(a.n, a.n_heads, a.batch);
+    self_f32_kernel<<<grid, 64, a.n * sizeof(float), stream>>>(a);
+    return hipGetLastError();
+}
 
 hipError_t launch_generic_causal(const flash_args& a, uint32_t q_dtype, hipStream_t stream) {
     const dim3 grid(a.n, a.n_heads, 1);

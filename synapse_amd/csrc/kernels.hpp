@@ -114,6 +114,7 @@ struct flash_args {
     uint32_t row;          // n_kv * hd
     uint32_t ctx_stride;
     float scale_log2e;
+    float scale;           // the f32 image kernel's own multiply
 };
 
 // Causal prefill over the cache (prefill.hip). Its buffer resources span the
@@ -128,6 +129,13 @@ hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStrea
 // causal over a cache, one query row per (token, head).
 hipError_t launch_generic_causal(const flash_args& a, uint32_t q_dtype, hipStream_t stream);
 hipError_t launch_generic_bidirectional(const flash_args& a, uint32_t in_dtype, hipStream_t stream);
+
+// Image-encoder attention on f32 rows in the reference's own f32 arithmetic
+// (no binary16 operands); images of up to self_f32_max_keys rows (the
+// probabilities of one query row sit in 64 KiB of LDS).
+constexpr uint32_t self_f32_max_keys = 16384;
+bool self_f32_fits(uint32_t n);
+hipError_t launch_self_f32(const flash_args& a, hipStream_t stream);
 
 // ---- RoPE -------------------------------------------------------------------
 struct rope_args {

@@ -66,6 +66,49 @@ __device__ __forceinline__ h8 pf_load_q(const void* base, std::size_t index) {
     }
 }
 
+// The P^T operands of one 64-key tile from its raw scores: p = exp2(s c - mc)
+// rounded to binary16. A query whose keys all lie in the first key tile
+// (position < pf_bk) takes its softmax whole there, as attend_group takes it
+// (S/kernels/attention.hpp:222-227): its max is the tile's, its sum the
+// tile's unrounded sum, and it rounds the normalised p = exp(s - max) / sum.
+// Returns true for such a query (its O is then complete and normalised, its
+// sum 1); later tiles hold none of its keys. Other queries keep the online
+// form: unnormalised p rounded, O divided by the sum of the rounded p at the
+// end. Only a wave whose first query sits in the first tile pays for the sum.
+__device__ __forceinline__ bool probabilities(uint32_t t0, uint32_t pos_row0, uint32_t my_pos, float mc,
+                                              f16v (&sc)[2], h8 (&pv)[4], float c) {
+    if (t0 == 0 && pos_row0 < pf_bk) {  // wave-uniform
+        float es = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                sc[e][i] = fast_exp2(sc[e][i] * c - mc);  // the scores are not needed again
+                es += sc[e][i];
+            }
+        }
+        es = sum32(es);
+        const bool whole = my_pos < pf_bk;
+        const float f = whole ? 1.0f / es : 1.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                pv[2 * e + (i >> 3)][i & 7] = to_h(sc[e][i] * f);
+            }
+        }
+        return whole;
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pv[2 * e + (i >> 3)][i & 7] = to_h(fast_exp2(sc[e][i] * c - mc));
+        }
+    }
+    return false;
+}
+
 template <int HD, bool QF16>
 __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const flash_args a) {
     constexpr int NS = HD / 16;     // k-steps of the score product
@@ -257,13 +300,7 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
         }
         const float mc = (m_run == -INFINITY ? 0.0f : m_run) * c;
         h8 pv[4];  // P^T operands: 16-key steps 0..3 of the tile
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                pv[2 * e + (i >> 3)][i & 7] = to_h(fast_exp2(sc[e][i] * c - mc));
-            }
-        }
+        const bool whole = probabilities(t0, a.pos + q_row0, my_pos, mc, sc, pv, c);
         float psum = 0.0f;
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
@@ -272,7 +309,8 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
                 psum = add_pair(h2{pv[s2][i], pv[s2][i + 1]}, psum);
             }
         }
-        l_run += sum32(psum);
+        psum = sum32(psum);
+        l_run = whole ? 1.0f : l_run + psum;
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
             const char* vrow = sv + ((32 * n + qi) * VROWC + H) * 16;  // V^T row 32n + qi, keys 8H..
@@ -597,13 +635,7 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
         }
         const float mc = (m_run == -INFINITY ? 0.0f : m_run) * c;
         h8 pv[4];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                pv[2 * e + (i >> 3)][i & 7] = to_h(fast_exp2(sc[e][i] * c - mc));
-            }
-        }
+        const bool whole = probabilities(t0, a.pos + q_row0, my_pos, mc, sc, pv, c);
         float psum = 0.0f;
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
@@ -612,7 +644,8 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
                 psum = add_pair(h2{pv[s2][i], pv[s2][i + 1]}, psum);
             }
         }
-        l_run += sum32(psum);
+        psum = sum32(psum);
+        l_run = whole ? 1.0f : l_run + psum;
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
             const char* vrow = sv + ((32 * n + qi) * VROWC + H) * 16;

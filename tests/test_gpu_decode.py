@@ -12,7 +12,7 @@ import pytest
 
 import binding as orc
 from gpu_util import SYN_F16, SYN_F32, Arena, attention, capi, scratch_for
-from helpers import assert_close
+from helpers import assert_close, assert_p_rounded_normalised
 from synapse_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
@@ -64,6 +64,17 @@ def test_decode_f16_query_matches_f32_query(arena):
 def test_decode_lengths_cross_split_edges(arena, ctx):
     got, want, _, _ = _case(arena, 32, 8, 128, ctx, seed=100 + ctx)
     assert_close(got, want, what=f"ctx {ctx}")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,ctx", [(4, 2, 16, 0), (4, 2, 16, 15), (32, 8, 128, 31), (32, 8, 128, 32),
+                                                (32, 8, 128, 100), (32, 8, 128, 127), (8, 4, 64, 64), (6, 3, 40, 90)])
+def test_decode_short_sequences_round_normalised_p(arena, n_heads, n_kv, hd, ctx):
+    """Up to 128 rows the kernel takes the softmax whole and rounds the
+    normalised p to binary16 where attend_group rounds it
+    (S/kernels/attention.hpp:222-227), so it follows the oracle to f32
+    rounding but for the odd weight that rounds the other way."""
+    got, want, _, _ = _case(arena, n_heads, n_kv, hd, ctx, seed=500 + ctx)
+    assert_p_rounded_normalised(got, want, n_heads, what=f"ctx {ctx}")
 
 
 @pytest.mark.parametrize("ctx", [70000, 150000])

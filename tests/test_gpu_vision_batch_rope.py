@@ -9,7 +9,7 @@ import pytest
 
 import binding as orc
 from gpu_util import SYN_F16, SYN_F32, Arena, SeqDesc, capi, check, lib, put_rows, self_attention, seq_array
-from helpers import assert_close
+from helpers import assert_close, assert_p_rounded_normalised
 from synapse_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
@@ -24,6 +24,12 @@ def arena():
 
 # ---- bidirectional ----------------------------------------------------------
 
+# f32 rows take a kernel with the reference's own f32 arithmetic: the same
+# fma chains in the same order as the oracle, so only the exponential's last
+# bits differ.
+F32_BOUND = 2e-6
+
+
 def _vision(arena, n, batch, n_heads, hd, dtype, sigma=0.5, seed=3, images=None):
     g = wl.rng(seed)
     shape = (batch * n, n_heads * hd)
@@ -36,6 +42,9 @@ def _vision(arena, n, batch, n_heads, hd, dtype, sigma=0.5, seed=3, images=None)
         sl = slice(b * n, (b + 1) * n)
         want = orc.self_attention(q[sl], k[sl], v[sl], n_heads, scale, threads=8)
         assert_close(got[sl], want, what=f"image {b} n={n} heads={n_heads} hd={hd}")
+        if dtype == SYN_F32:
+            err = np.abs(got[sl] - want).max() / np.abs(want).max()
+            assert err < F32_BOUND, (b, n, hd, err)
 
 
 def test_vision_clip_vit_l14(arena):
@@ -49,10 +58,26 @@ def test_vision_clip_vit_l14(arena):
                                   (288, 64), (289, 64), (577, 64), (128, 128), (129, 128), (31, 96)])
 def test_vision_shapes_f32_inputs(arena, n, hd):
     """The reference's self-attention cases (tests/sdk/kernels_vision.cpp:
-    200-250, n in {37, 1, 6, 13, 50}) with f32 inputs, which the kernel
-    rounds to binary16 for the matrix cores. The shapes cover both forms:
-    keys resident in LDS (n up to 288 at hd 64, 128 at hd 128) and tiled."""
+    200-250, n in {37, 1, 6, 13, 50}) and larger images with f32 inputs,
+    which keep the reference's f32 arithmetic: within F32_BOUND of the
+    oracle."""
     _vision(arena, n, 2, 3, hd, SYN_F32)
+
+
+def test_vision_f32_beyond_lds_rows(arena):
+    """f32 images longer than the f32 kernel's 16384 rows take the
+    matrix-core kernel, which rounds the operands to binary16 on load: four
+    query rows against a float64 softmax, within binary16's rounding."""
+    n, hd = 16400, 64
+    g = wl.rng(21)
+    q, k, v = (wl.normal(g, (n, hd), 0.5) for _ in range(3))
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    got = self_attention(arena, q, k, v, n, 1, 1, scale, SYN_F32)
+    for i in (0, 1, 8191, n - 1):
+        s = (q[i].astype(np.float64) @ k.astype(np.float64).T) * scale
+        p = np.exp(s - s.max())
+        want = (p / p.sum()) @ v.astype(np.float64)
+        assert np.abs(got[i] - want).max() < 2e-3 * np.abs(want).max() + 1e-4, i
 
 
 @pytest.mark.parametrize("n,hd", [(257, 64), (577, 64), (100, 128), (1, 64), (33, 32), (64, 64), (65, 64),
@@ -98,7 +123,14 @@ def _ragged(arena, lengths, n_heads, n_kv, hd, seed):
     for i, s in enumerate(seqs):
         got = arena.download(s.out_offset, (1, n_heads * hd), np.float32)
         assert_close(got, refs[i], what=f"sequence {i} (length {lengths[i]})")
+        if lengths[i] <= SHORT_ROWS:
+            assert_p_rounded_normalised(got, refs[i], n_heads, what=f"sequence {i} (length {lengths[i]})")
     arena.top = mark
+
+
+# A sequence of at most SHORT_ROWS rows rounds its normalised p to binary16,
+# as attend_group does.
+SHORT_ROWS = 128
 
 
 def test_ragged_decode_config4(arena):
@@ -108,7 +140,9 @@ def test_ragged_decode_config4(arena):
 
 
 def test_ragged_decode_many_short(arena):
-    """More sequences than one launch takes (32), lengths from 1 up."""
+    """More sequences than one launch takes (32), lengths from 1 up. Those
+    of at most 128 rows take the softmax whole, in a batch with longer ones
+    too, and round p where the oracle rounds it."""
     lengths = [1, 2, 31, 32, 33, 128, 129, 500] * 5
     _ragged(arena, lengths, 8, 2, 64, seed=4)
 

@@ -153,6 +153,69 @@ def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int,
                                "kernel_ms_mean_bracketed": float(np.mean(kern)), "graph_steps": reps * layers}
 
 
+def bench_decode_rope(hip: Hip, cfg: wl.Decode, steps: int, layers: int):
+    """Config 2 with Llama 3's RoPE applied to the step's q and k: the layer's
+    op_rope(q), op_rope(k) and op_attention as one syn_hip_attention_rope
+    call (the split kernel rotates in LDS; 2 launches) against the three
+    separate calls (4 launches). Same rotating KV states as bench_decode."""
+    row = cfg.n_kv * cfg.head_dim
+    max_ctx = cfg.ctx + 1
+    qsz = cfg.n_heads * cfg.head_dim
+    state = capi.kv_state_bytes(max_ctx, cfg.n_kv, cfg.head_dim)
+    scratch_bytes = int(lib().syn_hip_attention_scratch_bytes(cfg.n_heads, cfg.n_kv, cfg.head_dim, max_ctx, 1))
+    arena = Arena(layers * (state + 4 * capi.align(qsz * 4) + 4 * capi.align(row * 4)) + scratch_bytes + (1 << 20))
+    kc, vc, q, k, v = wl.decode_inputs(cfg)
+    scratch = arena.alloc(scratch_bytes)
+    theta_scale = float(np.float32(cfg.theta) ** np.float32(-2.0 / cfg.head_dim))
+    rope = dict(freq_factors_offset=capi.NO_OFFSET, theta_scale=theta_scale, mode=0, freq_scale=1.0,
+                ext_factor=0.0, attn_factor=1.0, corr_low=0.0, corr_high=0.0)
+    fused, separate = [], []
+    for _ in range(layers):
+        cache = capi.kv_state(arena, max_ctx, cfg.n_kv, cfg.head_dim)
+        capi.upload_cache(arena, cache, kc, vc)
+        q_off, k_off, v_off = arena.put(q), arena.put(k), arena.put(v)
+        qr, kr, out = arena.alloc(qsz * 4), arena.alloc(row * 4), arena.alloc(qsz * 4)
+        d = AttnDesc(cache=cache, q_offset=q_off, k_offset=k_off, v_offset=v_off, out_offset=out,
+                     scratch_offset=scratch, scratch_bytes=scratch_bytes, n_heads=cfg.n_heads, pos=cfg.ctx, n=1,
+                     scale=cfg.scale, q_dtype=SYN_F32, kv_dtype=SYN_F32)
+        r = capi.AttnRopeDesc(q_out_offset=qr, k_out_offset=kr, temp_scale=0.0, temp_floor_len=0, **rope)
+        fused.append((ctypes.byref(d), ctypes.byref(r)))
+        rq = capi.RopeDesc(in_offset=q_off, out_offset=qr, n=1, size=qsz, head_dim=cfg.head_dim, pos=cfg.ctx, **rope)
+        rk = capi.RopeDesc(in_offset=k_off, out_offset=kr, n=1, size=row, head_dim=cfg.head_dim, pos=cfg.ctx, **rope)
+        d2 = AttnDesc(cache=cache, q_offset=qr, k_offset=kr, v_offset=v_off, out_offset=out,
+                      scratch_offset=scratch, scratch_bytes=scratch_bytes, n_heads=cfg.n_heads, pos=cfg.ctx, n=1,
+                      scale=cfg.scale, q_dtype=SYN_F32, kv_dtype=SYN_F32)
+        separate.append((ctypes.byref(rq), ctypes.byref(rk), ctypes.byref(d2), d2))
+    L = lib()
+    stream = arena.stream
+
+    def run_fused(i):
+        check(L.syn_hip_attention_rope(arena.handle, *fused[i % layers]))
+
+    def run_separate(i):
+        rq, rk, d2, _ = separate[i % layers]
+        check(L.syn_hip_rope(arena.handle, rq))
+        check(L.syn_hip_rope(arena.handle, rk))
+        check(L.syn_hip_attention(arena.handle, d2))
+
+    result = {}
+    for name, fn in (("fused_us", run_fused), ("separate_us", run_separate)):
+        for i in range(2 * layers):
+            fn(i)
+        arena.sync()
+        t0, t1 = hip.events(2)
+        hip.record(t0, stream)
+        for i in range(steps):
+            fn(i)
+        hip.record(t1, stream)
+        result[name] = round(hip.ms(t0, t1) / steps * 1e3, 3)
+    out = arena.download(separate[0][3].out_offset, (qsz,), np.float32)
+    assert np.all(np.isfinite(out))
+    arena.close()
+    result.update({"launches_fused": 2, "launches_separate": 4, "steps": steps})
+    return result
+
+
 def bench_prefill(hip: Hip, cfg: wl.Prefill, reps: int):
     """Config 3: the flash kernel alone (cache already appended) and the
     whole op (append + attend)."""
@@ -497,6 +560,8 @@ def main() -> int:
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
     replay = f" ({graph_ms * 1e3:.2f} us/step replayed from a HIP graph)" if graph_ms is not None else ""
     log(f"decode: {step_ms * 1e3:.2f} us/step -> {value:.0f} GB/s{replay}")
+    extra["decode_rope"] = bench_decode_rope(hip, cfg, 400, args.layers)
+    log(f"decode with RoPE: {extra['decode_rope']}")
     extra.update({"decode_step_us": round(step_ms * 1e3, 3),
                   "decode_graph_step_us": round(graph_ms * 1e3, 3) if graph_ms is not None else None,
                   "decode_tokens_per_s_32_layers": round(1e3 / (step_ms * 32), 1),

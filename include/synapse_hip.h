@@ -171,8 +171,10 @@ int syn_hip_attend_batch(syn_arena* arena, const syn_seq_desc* seqs, uint32_t n_
  * and head h, out_i,h = softmax_j(scale * q_i,h . k_j,h) v_j,h over j = 0..n-1.
  * Rows are grouped into `batch` independent images of n rows each (the
  * reference runs one image per run_rows call, S/models/clip.hpp:405-416).
- * Operands are rounded to binary16 for the matrix cores; softmax and
- * accumulation in f32, f32 output. */
+ * f32 rows of images up to 16384 rows keep the reference's f32 arithmetic
+ * (its fma chains, in its order); f16 rows, and longer f32 images, go to the
+ * matrix cores as binary16 operands with binary16 probabilities. Softmax
+ * and accumulation in f32, f32 output. */
 typedef struct syn_self_desc {
     uint64_t q_offset;   /* batch*n rows of n_heads*head_dim, type in_dtype */
     uint64_t k_offset;
@@ -200,7 +202,7 @@ typedef struct syn_rope_desc {
     uint64_t freq_factors_offset; /* head_dim/2 f32, or UINT64_MAX for none */
     uint32_t n;
     uint32_t size;                /* a multiple of head_dim */
-    uint32_t head_dim;            /* even */
+    uint32_t head_dim;            /* even, <= 256 */
     uint32_t pos;
     float theta_scale;            /* base^(-2/head_dim) */
     uint32_t mode;                /* 0 normal, 1 neox */
@@ -208,6 +210,46 @@ typedef struct syn_rope_desc {
 } syn_rope_desc;
 
 int syn_hip_rope(syn_arena* arena, const syn_rope_desc* desc);
+
+/* op_attn_temperature over n rows in one launch (S/graph/session.hpp:343-347):
+ * row i times t(pos + i), t(p) = float(log(floor(float(p) / floor_len) + 1)
+ * * scale + 1) with the logarithm in double (kernels::attn_temperature,
+ * S/kernels/elementwise.hpp:66-72), computed on the device per row. */
+typedef struct syn_temperature_desc {
+    uint64_t in_offset;  /* n rows of size f32 */
+    uint64_t out_offset; /* n rows of size f32; may alias in */
+    uint32_t n;
+    uint32_t size;
+    uint32_t pos;        /* position of row 0 */
+    uint32_t floor_len;  /* >= 1 */
+    float scale;
+    uint32_t reserved;
+} syn_temperature_desc;
+
+int syn_hip_attn_temperature(syn_arena* arena, const syn_temperature_desc* desc);
+
+/* One layer's op_rope on q, op_rope on k, op_attn_temperature on q (when
+ * temp_floor_len != 0) and op_attention (S/graph/session.hpp:337-374, four
+ * ops in the reference) as one call; desc's q_offset and k_offset hold the
+ * rows before RoPE, f32. A single-token step that the split-KV decode
+ * kernel takes is that one kernel: it rotates q and the new K row in LDS
+ * with syn_hip_rope's arithmetic, multiplies q by the temperature, stores
+ * the rotated K row into the cache, and writes no rotated rows -- equal, bit
+ * for bit, to the separate calls. Any other run makes the separate calls:
+ * rotated (and scaled) q rows to q_out_offset, rotated k rows to
+ * k_out_offset, then syn_hip_attention on them. */
+typedef struct syn_attn_rope_desc {
+    uint64_t q_out_offset;        /* n rows of n_heads*head_dim f32 (runs that do not fuse) */
+    uint64_t k_out_offset;        /* n rows of n_kv_heads*head_dim f32 (likewise) */
+    uint64_t freq_factors_offset; /* head_dim/2 f32 (16-byte aligned), or UINT64_MAX for none */
+    float theta_scale;
+    uint32_t mode;                /* 0 normal, 1 neox */
+    float freq_scale, ext_factor, attn_factor, corr_low, corr_high;
+    float temp_scale;             /* op_attn_temperature's scale */
+    uint32_t temp_floor_len;      /* its floor length; 0: no temperature */
+} syn_attn_rope_desc;
+
+int syn_hip_attention_rope(syn_arena* arena, const syn_attn_desc* desc, const syn_attn_rope_desc* rope);
 
 /* ---- the rest of a Llama-family decode graph ---------------------------------
  * With syn_hip_rope and syn_hip_attention these run a whole layer stack from

@@ -84,6 +84,8 @@ CPP_TESTS = {
     "test_session": ("tests/cpp/test_session.cpp", True),
     "test_model_session": ("tests/cpp/test_model_session.cpp", False),
 }
+# Host builds of device-side math (no library, no HIP).
+CPP_MATH_TESTS = {"test_rope_math": "tests/cpp/test_rope_math.cpp"}
 # Host tests linked against tests/cpp/stub_abi.cpp (a C ABI that launches
 # nothing) instead of the library: they run on the CPU.
 CPP_STUB_TESTS = {"test_no_alloc": "tests/cpp/test_no_alloc.cpp"}
@@ -101,6 +103,9 @@ def build_host_tests() -> None:
         if oracle:
             cmd += [f"-I{ROOT / 'oracle'}", f"-L{ROOT / 'oracle'}", "-loracle", f"-Wl,-rpath,{ROOT / 'oracle'}"]
         _run(cmd)
+    for name, src in CPP_MATH_TESTS.items():
+        _run(["g++", "-std=c++20", "-O2", "-Wall", "-Wextra", "-Werror", "-Wno-unknown-pragmas", "-ffp-contract=off", f"-I{CSRC}",
+              f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / src), "-o", str(out / name)])
     for name, src in CPP_STUB_TESTS.items():
         _run(["g++", "-std=c++20", "-O2", "-Wall", "-Wextra", "-Werror", "-ffp-contract=off", f"-I{HOST_INC}",
               f"-I{ROOT / 'include'}", f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / src),

@@ -47,6 +47,17 @@ class RopeDesc(ctypes.Structure):
                 ("ext_factor", f32), ("attn_factor", f32), ("corr_low", f32), ("corr_high", f32)]
 
 
+class AttnRopeDesc(ctypes.Structure):
+    _fields_ = [("q_out_offset", u64), ("k_out_offset", u64), ("freq_factors_offset", u64), ("theta_scale", f32),
+                ("mode", u32), ("freq_scale", f32), ("ext_factor", f32), ("attn_factor", f32), ("corr_low", f32),
+                ("corr_high", f32), ("temp_scale", f32), ("temp_floor_len", u32)]
+
+
+class TemperatureDesc(ctypes.Structure):
+    _fields_ = [("in_offset", u64), ("out_offset", u64), ("n", u32), ("size", u32), ("pos", u32),
+                ("floor_len", u32), ("scale", f32), ("reserved", u32)]
+
+
 class EmbedDesc(ctypes.Structure):
     _fields_ = [("table_offset", u64), ("out_offset", u64), ("n_table_rows", u32), ("size", u32),
                 ("table_type", u32), ("reserved", u32)]
@@ -114,6 +125,8 @@ SIGNATURES = {
     "syn_hip_attend_batch": (i32, [ctypes.c_void_p, ctypes.POINTER(SeqDesc), u32, u32, f32, u32, u64, u64]),
     "syn_hip_self_attention": (i32, [ctypes.c_void_p, ctypes.POINTER(SelfDesc)]),
     "syn_hip_rope": (i32, [ctypes.c_void_p, ctypes.POINTER(RopeDesc)]),
+    "syn_hip_attn_temperature": (i32, [ctypes.c_void_p, ctypes.POINTER(TemperatureDesc)]),
+    "syn_hip_attention_rope": (i32, [ctypes.c_void_p, ctypes.POINTER(AttnDesc), ctypes.POINTER(AttnRopeDesc)]),
     "syn_hip_embed": (i32, [ctypes.c_void_p, ctypes.POINTER(EmbedDesc), ctypes.POINTER(u32), u32]),
     "syn_hip_rms_norm": (i32, [ctypes.c_void_p, ctypes.POINTER(NormDesc)]),
     "syn_hip_matmul": (i32, [ctypes.c_void_p, ctypes.POINTER(MatmulDesc)]),

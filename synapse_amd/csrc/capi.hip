@@ -168,7 +168,8 @@ struct partial_area {
 // One decode launch over seqs[0..n): fills the argument block, checks the
 // scratch, launches. kv_dtype types the sequences' k_new / v_new rows.
 int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n_kv, uint32_t hd, uint32_t group,
-               float scale, uint32_t q_dtype, uint32_t kv_dtype, const partial_area& pa) {
+               float scale, uint32_t q_dtype, uint32_t kv_dtype, const partial_area& pa,
+               const syn::rope_params* rope = nullptr) {
     if (n == 0 || n > syn::decode_max_seqs) {
         return fail(SYN_HIP_EINVAL, "decode: %u sequences in one launch", n);
     }
@@ -227,6 +228,10 @@ int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n
             }
             prm.part = reinterpret_cast<float*>(a->base + pa.arena_offset);
         }
+    }
+    if (n == 1 && rope != nullptr) {
+        syn::decode_rope_args one{prm, table[0], *rope};
+        return hip_status(syn::launch_decode(one, q_dtype, a->stream), "decode launch");
     }
     if (n == 1) {
         syn::decode_one_args one{prm, table[0]};
@@ -317,7 +322,8 @@ bool decode_shape(const syn_attn_desc* d) {
 
 // Attends the run; with_new_rows, a single-token step's K, V row is appended
 // by the decode kernel itself (one launch), longer runs were appended before.
-int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows, const partial_area* static_area = nullptr) {
+int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows, const partial_area* static_area = nullptr,
+                   const syn::rope_params* rope = nullptr) {
     const syn_kv_desc& c = d->cache;
     const uint32_t group = d->n_heads / c.n_kv_heads;
     if (decode_shape(d)) {
@@ -334,7 +340,7 @@ int attend_checked(syn_arena* a, const syn_attn_desc* d, bool with_new_rows, con
         s.ctx_stride = c.ctx_stride;
         const partial_area arena_area{d->scratch_offset, d->scratch_bytes, nullptr};
         return run_decode(a, &s, 1, c.n_kv_heads, c.head_dim, group, d->scale, d->q_dtype, d->kv_dtype,
-                          static_area != nullptr ? *static_area : arena_area);
+                          static_area != nullptr ? *static_area : arena_area, rope);
     }
     const syn::flash_args f = flash_of(a, d);
     if (fast_shape(c.head_dim) && (uint64_t{d->n} + 127) / 128 <= 65535 &&
@@ -590,6 +596,110 @@ int syn_hip_attention_noalloc(syn_arena* a, const syn_attn_desc* d) {
     return attend_checked(a, d, true, &area);
 }
 
+int syn_hip_attn_temperature(syn_arena* a, const syn_temperature_desc* d) {
+    if (int e = check_arena(a)) {
+        return e;
+    }
+    if (d == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null descriptor");
+    }
+    if (d->floor_len == 0 || d->size == 0) {
+        return fail(SYN_HIP_EINVAL, "attn_temperature: size %u, floor_len %u", d->size, d->floor_len);
+    }
+    if (d->n == 0) {
+        return SYN_HIP_OK;
+    }
+    const uint64_t bytes = uint64_t{d->n} * d->size * 4;
+    if (int e = check_range(a, d->in_offset, bytes, 4, "attn_temperature in")) {
+        return e;
+    }
+    if (int e = check_range(a, d->out_offset, bytes, 4, "attn_temperature out")) {
+        return e;
+    }
+    return hip_status(syn::launch_attn_temperature(reinterpret_cast<const float*>(a->base + d->in_offset),
+                                                   reinterpret_cast<float*>(a->base + d->out_offset), d->n, d->size,
+                                                   d->pos, d->floor_len, d->scale, a->stream),
+                      "attn_temperature launch");
+}
+
+int syn_hip_attention_rope(syn_arena* a, const syn_attn_desc* d, const syn_attn_rope_desc* r) {
+    if (int e = check_attn(a, d, true)) {
+        return e;
+    }
+    if (r == nullptr) {
+        return fail(SYN_HIP_EINVAL, "null RoPE descriptor");
+    }
+    const syn_kv_desc& c = d->cache;
+    if (d->q_dtype != SYN_F32 || d->kv_dtype != SYN_F32 || c.head_dim % 2 != 0 || r->mode > 1 ||
+        c.head_dim > 2 * syn::rope_max_pairs) {
+        return fail(SYN_HIP_EINVAL, "attention_rope: q dtype %u, k dtype %u (want f32), head_dim %u, mode %u",
+                    d->q_dtype, d->kv_dtype, c.head_dim, r->mode);
+    }
+    const float* ff = nullptr;
+    if (r->freq_factors_offset != no_offset) {
+        if (int e = check_range(a, r->freq_factors_offset, uint64_t{c.head_dim} / 2 * 4, 16, "rope freq_factors")) {
+            return e;
+        }
+        ff = reinterpret_cast<const float*>(a->base + r->freq_factors_offset);
+    }
+    if (decode_shape(d)) {
+        // One kernel: q and the new K row rotated in LDS, the K row appended.
+        syn::rope_params rp{};
+        rp.freq_factors = ff;
+        rp.mode = r->mode;
+        rp.theta_scale = r->theta_scale;
+        rp.freq_scale = r->freq_scale;
+        rp.ext_factor = r->ext_factor;
+        rp.attn_factor = r->attn_factor;
+        rp.corr_low = r->corr_low;
+        rp.corr_high = r->corr_high;
+        rp.q_scale = r->temp_floor_len != 0 ? syn::attn_temperature(d->pos, r->temp_scale, r->temp_floor_len) : 1.0f;
+        return attend_checked(a, d, true, nullptr, &rp);
+    }
+    // The separate ops, into the caller's rows.
+    syn_rope_desc rd{};
+    rd.freq_factors_offset = r->freq_factors_offset;
+    rd.n = d->n;
+    rd.head_dim = c.head_dim;
+    rd.pos = d->pos;
+    rd.theta_scale = r->theta_scale;
+    rd.mode = r->mode;
+    rd.freq_scale = r->freq_scale;
+    rd.ext_factor = r->ext_factor;
+    rd.attn_factor = r->attn_factor;
+    rd.corr_low = r->corr_low;
+    rd.corr_high = r->corr_high;
+    rd.in_offset = d->q_offset;
+    rd.out_offset = r->q_out_offset;
+    rd.size = d->n_heads * c.head_dim;
+    if (int e = syn_hip_rope(a, &rd)) {
+        return e;
+    }
+    if (r->temp_floor_len != 0) {
+        syn_temperature_desc td{};
+        td.in_offset = r->q_out_offset;
+        td.out_offset = r->q_out_offset;
+        td.n = d->n;
+        td.size = rd.size;
+        td.pos = d->pos;
+        td.floor_len = r->temp_floor_len;
+        td.scale = r->temp_scale;
+        if (int e = syn_hip_attn_temperature(a, &td)) {
+            return e;
+        }
+    }
+    rd.in_offset = d->k_offset;
+    rd.out_offset = r->k_out_offset;
+    rd.size = c.n_kv_heads * c.head_dim;
+    if (int e = syn_hip_rope(a, &rd)) {
+        return e;
+    }
+    syn_attn_desc rotated = *d;
+    rotated.q_offset = r->q_out_offset;
+    rotated.k_offset = r->k_out_offset;
+    return syn_hip_attention(a, &rotated);
+}
+
 uint64_t syn_hip_attention_noalloc_scratch_limit(void) {
     return noalloc_scratch_bytes;
 }
@@ -784,8 +894,10 @@ int syn_hip_rope(syn_arena* a, const syn_rope_desc* d) {
     if (d == nullptr) {
         return fail(SYN_HIP_EINVAL, "null descriptor");
     }
-    if (d->head_dim == 0 || d->head_dim % 2 != 0 || d->size == 0 || d->size % d->head_dim != 0 || d->mode > 1) {
-        return fail(SYN_HIP_EINVAL, "rope: size %u, head_dim %u, mode %u", d->size, d->head_dim, d->mode);
+    if (d->head_dim == 0 || d->head_dim % 2 != 0 || d->head_dim > 2 * syn::rope_max_pairs || d->size == 0 ||
+        d->size % d->head_dim != 0 || d->mode > 1) {
+        return fail(SYN_HIP_EINVAL, "rope: size %u, head_dim %u (even, <= 256), mode %u", d->size, d->head_dim,
+                    d->mode);
     }
     if (d->n == 0) {
         return SYN_HIP_OK;

@@ -86,6 +86,13 @@ struct decode_traits<decode_one_args> {
     __device__ static uint32_t find_merge(const decode_one_args&, uint32_t) { return 0; }
 };
 template <>
+struct decode_traits<decode_rope_args> {
+    static constexpr bool multi = false;
+    __host__ __device__ static const decode_seq& seq(const decode_rope_args& a, uint32_t) { return a.s; }
+    __device__ static uint32_t find(const decode_rope_args&, uint32_t) { return 0; }
+    __device__ static uint32_t find_merge(const decode_rope_args&, uint32_t) { return 0; }
+};
+template <>
 struct decode_traits<decode_batch_args> {
     static constexpr bool multi = true;
     __host__ __device__ static const decode_seq& seq(const decode_batch_args& a, uint32_t i) { return a.seq[i]; }
@@ -98,16 +105,20 @@ struct decode_traits<decode_batch_args> {
 };
 
 // LDS of the split kernel: the group's q as given (f32 size, the larger),
-// the new K and V row of one head (likewise), per-wave (max, sum), then the
-// waves' unscaled outputs, head rows padded by 4 floats.
+// the new K and V row of one head (likewise), per-wave (max, sum), the
+// waves' unscaled outputs (head rows padded by 4 floats), then a fused
+// step's RoPE table (hd/2 cos, hd/2 sin) and frequency factors (a 1 KB copy).
 inline __host__ __device__ uint32_t q_lds_bytes(uint32_t group, uint32_t hd) {
     return (group * hd * 4 + 15) / 16 * 16;
 }
 inline __host__ __device__ uint32_t new_lds_bytes(uint32_t hd) {
     return (2 * hd * 4 + 15) / 16 * 16;
 }
+inline __host__ __device__ uint32_t rope_lds_offset(uint32_t group, uint32_t hd) {
+    return q_lds_bytes(group, hd) + new_lds_bytes(hd) + (4 * 16 * 2 + 4 * group * (hd + 4)) * 4;
+}
 inline std::size_t decode_lds_bytes(uint32_t group, uint32_t hd) {
-    return q_lds_bytes(group, hd) + new_lds_bytes(hd) + (4 * 16 * 2 + 4 * std::size_t{group} * (hd + 4)) * sizeof(float);
+    return rope_lds_offset(group, hd) + std::size_t{hd} * sizeof(float) + 1024;
 }
 
 // s_waitcnt immediate that waits until at most n vector memory operations
@@ -117,6 +128,16 @@ constexpr int vmcnt_imm(int n) {
     return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8);
 }
 
+// The fused step's RoPE fields (other launches have none and never use them).
+template <class A>
+__device__ __forceinline__ const rope_params& a_rope(const A& a) {
+    if constexpr (std::is_same_v<A, decode_rope_args>) {
+        return a.r;
+    } else {
+        __builtin_unreachable();
+    }
+}
+
 // SHORT: some sequence of the launch has at most decode_chunk_unit rows and
 // takes the whole-softmax path below; launches without one compile it out
 // (it costs the online path about 60 registers).
@@ -124,6 +145,8 @@ template <int HDP, bool QF16, bool SHORT, class A>
 __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     using T = decode_traits<A>;
     constexpr bool MULTI = T::multi;
+    constexpr bool ROPE = std::is_same_v<A, decode_rope_args>;
+    static_assert(!(ROPE && QF16), "a fused RoPE step takes f32 q");
     const decode_params& p = a.p;
     constexpr int NS = HDP / 32;   // k-steps of the score product
     constexpr int NT = HDP / 16;   // 16-dim tiles of the output
@@ -157,7 +180,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // from k_new / v_new, rounded to binary16, and store it into the cache.
     const uint32_t new_t = s.len - 1;
     const bool new_here = s.k_new != nullptr && t_end == s.len;
-    const bool kv_f16 = p.kv_dtype == 1;
+    const bool kv_f16 = !ROPE && p.kv_dtype == 1;  // a fused RoPE step takes f32 rows
 
     // Every K, V load below is unconditional, so a wave issues all of them
     // back to back: a lane with nothing to read points at valid data and
@@ -240,6 +263,36 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // q^T operand: lane (G, r) holds head h0 + r, dims 32*st + 8*G + [0, 8),
     // rounded to binary16 as attend_group rounds q (S/kernels/attention.hpp:204-206).
     h8 qv[NS];
+    // A fused RoPE step rotates the q rows and the new K row in LDS, once per
+    // block, after they have landed: wave 0 first builds every pair's cos
+    // and sin into a table, then the pairs of every row are rotated in place
+    // (q also times the temperature factor), and the staging below reads the
+    // rotated f32 rows as it reads unrotated ones.
+    float* rope_tab = reinterpret_cast<float*>(lds_bytes + rope_lds_offset(group, hd));
+    float rope_th0 = 0.0f, rope_th1 = 0.0f;  // wave 0: the angles of pairs ln and ln + 64
+    char* ff_lds = lds_bytes + rope_lds_offset(group, hd) + hd * 4;
+    const auto rope_rows = [&]() {
+        const uint32_t half = hd / 2;
+        if (w == 0) {
+            const float* ff = a_rope(a).freq_factors != nullptr ? reinterpret_cast<const float*>(ff_lds) : nullptr;
+            rope_table(a_rope(a), rope_th0, rope_th1, half, ff, rope_tab, static_cast<uint32_t>(ln));
+        }
+        lds_barrier();
+        const bool normal = a_rope(a).mode == 0;
+        const uint32_t rows = group + (new_here ? 1u : 0u);  // q heads, then the new K row
+        for (uint32_t u = tid; u < rows * half; u += 256) {
+            const uint32_t row = u / half;
+            const uint32_t pr = u % half;
+            float* x = row < group ? reinterpret_cast<float*>(lds_bytes) + row * hd : reinterpret_cast<float*>(new_lds);
+            const float f = row < group ? a_rope(a).q_scale : 1.0f;
+            const uint32_t i0 = normal ? 2 * pr : pr;
+            const uint32_t i1 = normal ? i0 + 1 : pr + half;
+            const float cs = rope_tab[pr], sn = rope_tab[half + pr];
+            const float x0 = x[i0], x1 = x[i1];
+            x[i0] = rope_first(x0, x1, cs, sn) * f;
+            x[i1] = rope_second(x0, x1, cs, sn) * f;
+        }
+    };
     const auto convert_q = [&](bool kv_issued) {
         // Wait for this wave's copies (q, the new row) only: the K, V loads
         // issued after them stay in flight. A wave with no positions issued
@@ -253,6 +306,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NS + NT));
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
+        if constexpr (ROPE) {
+            rope_rows();
         }
         lds_barrier();
 #pragma unroll
@@ -412,8 +468,25 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     constexpr uint32_t stride = decode_positions_per_wave * decode_waves;
     u4 kr[2][NS], vr[NT];
     uint32_t tb = t_begin + decode_positions_per_wave * w;
+    if constexpr (ROPE) {
+        // A fused step's frequency factors (hd/2 floats, at most 512 bytes)
+        // land in LDS with q, in wave 0's copy, which builds the table: its
+        // wait for q covers them. Lanes past the end re-read byte 0 into the
+        // area's slack.
+        if (w == 0 && a.r.freq_factors != nullptr) {
+            const uint32_t off = 16 * ln < 2 * hd ? 16 * ln : 0;
+            load16_lds(reinterpret_cast<const char*>(a.r.freq_factors) + off, ff_lds);
+        }
+    }
     if (tb < t_end) {
         load_kv(tb, kr, vr);
+    }
+    if constexpr (ROPE) {
+        // The angles need neither q nor the factors: wave 0 runs their
+        // chain while the loads are in flight.
+        if (w == 0) {
+            rope_thetas(new_t, a.r.theta_scale, hd / 2, static_cast<uint32_t>(ln), rope_th0, rope_th1);
+        }
     }
     convert_q(tb < t_end);
     float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));
@@ -686,9 +759,18 @@ hipError_t launch_hdp(const A& a, uint32_t q_dtype, hipStream_t stream) {
     for (uint32_t i = 0; i < a.p.n_seqs; ++i) {
         any_short = any_short || decode_traits<A>::seq(a, i).len <= decode_chunk_unit;
     }
-    const auto kernel = q_dtype == 1 ? (any_short ? decode_kernel<HDP, true, true, A> : decode_kernel<HDP, true, false, A>)
-                                     : (any_short ? decode_kernel<HDP, false, true, A> : decode_kernel<HDP, false, false, A>);
-    kernel<<<grid, 256, lds, stream>>>(a);
+    if constexpr (std::is_same_v<A, decode_rope_args>) {
+        if (q_dtype != 0) {
+            return hipErrorInvalidValue;
+        }
+        const auto kernel = any_short ? decode_kernel<HDP, false, true, A> : decode_kernel<HDP, false, false, A>;
+        kernel<<<grid, 256, lds, stream>>>(a);
+    } else {
+        const auto kernel = q_dtype == 1
+                                ? (any_short ? decode_kernel<HDP, true, true, A> : decode_kernel<HDP, true, false, A>)
+                                : (any_short ? decode_kernel<HDP, false, true, A> : decode_kernel<HDP, false, false, A>);
+        kernel<<<grid, 256, lds, stream>>>(a);
+    }
     if (a.p.merge_blocks > 0) {
         decode_merge_kernel<A><<<a.p.merge_blocks, 256, 0, stream>>>(a);
     }
@@ -739,6 +821,10 @@ hipError_t launch_decode(const decode_one_args& a, uint32_t q_dtype, hipStream_t
 }
 
 hipError_t launch_decode(const decode_batch_args& a, uint32_t q_dtype, hipStream_t stream) {
+    return launch_any(a, q_dtype, stream);
+}
+
+hipError_t launch_decode(const decode_rope_args& a, uint32_t q_dtype, hipStream_t stream) {
     return launch_any(a, q_dtype, stream);
 }
 

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "device.hpp"
+#include "rope_math.hpp"
 
 #include <cstddef>
 #include <cstdint>
@@ -76,6 +77,107 @@ struct decode_batch_args {
     uint32_t block0s[decode_max_seqs];  // seq[i].block0, contiguous: a block finds its sequence in one load batch
     uint32_t merge0s[decode_max_seqs];  // seq[i].merge0, likewise for the merge kernel
 };
+
+// RoPE and the attention temperature inside a single-sequence decode step:
+// the step's q row and new K row are rotated as op_rope rotates them
+// (S/kernels/attention.hpp:89-129), then q is multiplied by q_scale
+// (op_attn_temperature's factor at the step's position, S/kernels/
+// elementwise.hpp:66-72; 1 for none), before q's rounding to binary16. The
+// same arithmetic as the rope kernel, so the fused step equals the unfused
+// one bit for bit. q and the new rows are f32.
+struct rope_params {
+    const float* freq_factors;  // head_dim / 2 floats, or nullptr
+    uint32_t mode;              // 0 normal (pairs 2i, 2i + 1), 1 neox (pairs i, i + hd/2)
+    float theta_scale, freq_scale, ext_factor, attn_factor, corr_low, corr_high;
+    float q_scale;
+};
+
+struct decode_rope_args {
+    decode_params p;
+    decode_seq s;
+    rope_params r;
+};
+hipError_t launch_decode(const decode_rope_args& a, uint32_t q_dtype, hipStream_t stream);
+
+
+constexpr uint32_t rope_max_pairs = 128;  // head_dim <= 256, as attention's
+
+// The angles of RoPE pairs p0 = lane and p1 = lane + 64 at position pos, as
+// rope() builds them (S/kernels/attention.hpp:101-127): pos times theta_scale
+// p times over by repeated f32 multiplication (not pow), so each angle is
+// the reference's to the last bit. Every lane runs the same chain over all
+// n_pairs (uniform control flow: a chain per lane of its own length was a
+// divergent loop that cost microseconds) and keeps the values at its pairs.
+__device__ inline void rope_thetas(uint32_t pos, float theta_scale, uint32_t n_pairs, uint32_t lane, float& t0,
+                                   float& t1) {
+#pragma clang fp contract(off)
+    float th = static_cast<float>(pos);
+    t0 = th;
+    t1 = th;
+#pragma unroll 8
+    for (uint32_t j = 1; j < n_pairs; ++j) {
+        th *= theta_scale;
+        t0 = j == lane ? th : t0;
+        t1 = j == lane + 64 ? th : t1;
+    }
+}
+
+// cos and sin of RoPE pair p with angle theta (rope_thetas), times the YaRN
+// magnitude, as rope() computes them (S/kernels/attention.hpp:101-121): every
+// product and sum rounds on its own; cos and sin of the f32 angle from
+// sincos_of. R has the fields of rope_params (theta_scale .. corr_high).
+template <class R>
+__device__ inline void rope_coeffs(const R& r, float theta, uint32_t p, float ff, float& cs, float& sn) {
+#pragma clang fp contract(off)
+    const float theta_extrap = theta / ff;
+    const float theta_interp = r.freq_scale * theta_extrap;
+    float t = theta_interp;
+    float mscale = r.attn_factor;
+    if (r.ext_factor != 0.0f) {
+        const float yv = (static_cast<float>(p) - r.corr_low) / fmaxf(0.001f, r.corr_high - r.corr_low);
+        const float ramp_mix = (1 - fminf(1.0f, fmaxf(0.0f, yv))) * r.ext_factor;
+        t = theta_interp * (1 - ramp_mix) + theta_extrap * ramp_mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / r.freq_scale);
+    }
+    float c1, s1;
+    sincos_of(t, s1, c1);
+    cs = c1 * mscale;
+    sn = s1 * mscale;
+}
+
+// One wave builds the cos / sin table of every pair (n_pairs <= 128) into
+// tab[0 .. n_pairs) / tab[n_pairs .. 2 n_pairs) from the angles rope_thetas
+// gave its lanes; ff, if not null, holds the pairs' frequency factors.
+template <class R>
+__device__ inline void rope_table(const R& r, float th0, float th1, uint32_t n_pairs, const float* ff, float* tab,
+                                  uint32_t lane) {
+    if (lane < n_pairs) {
+        rope_coeffs(r, th0, lane, ff ? ff[lane] : 1.0f, tab[lane], tab[n_pairs + lane]);
+    }
+    if (lane + 64 < n_pairs) {
+        rope_coeffs(r, th1, lane + 64, ff ? ff[lane + 64] : 1.0f, tab[lane + 64], tab[n_pairs + lane + 64]);
+    }
+}
+
+// The rotated pair: (x0 cs - x1 sn, x0 sn + x1 cs), each product and sum
+// rounded on its own (S/kernels/attention.hpp:122-125).
+__device__ __forceinline__ float rope_first(float x0, float x1, float cs, float sn) {
+#pragma clang fp contract(off)
+    return x0 * cs - x1 * sn;
+}
+__device__ __forceinline__ float rope_second(float x0, float x1, float cs, float sn) {
+#pragma clang fp contract(off)
+    return x0 * sn + x1 * cs;
+}
+
+// The attention temperature of position pos (kernels::attn_temperature,
+// S/kernels/elementwise.hpp:66-72): a float quotient floored, the logarithm
+// in double, the result rounded to float. The same expression on the host
+// (the fused decode step's factor) and on the device (the row kernel).
+__host__ __device__ inline float attn_temperature(uint32_t pos, float scale, uint32_t floor_len) {
+    const float q = floorf(static_cast<float>(pos) / static_cast<float>(floor_len));
+    return static_cast<float>(log(static_cast<double>(q) + 1.0) * static_cast<double>(scale) + 1.0);
+}
 
 // Scratch floats one split contributes: (max, sum, output) for each head.
 inline std::size_t decode_split_floats(uint32_t group, uint32_t hd) {
@@ -168,6 +270,9 @@ hipError_t launch_rms_norm(const float* in, const float* gamma, float* out, uint
                            hipStream_t stream);
 hipError_t launch_matmul(const float* w, const float* x, const float* bias, float* out, uint32_t n, uint32_t rows,
                          uint32_t cols, hipStream_t stream);
+// op_attn_temperature over n rows at positions pos.. in one launch.
+hipError_t launch_attn_temperature(const float* in, float* out, uint32_t n, uint32_t size, uint32_t pos,
+                                   uint32_t floor_len, float scale, hipStream_t stream);
 hipError_t launch_elementwise(const float* a, const float* b, float* out, uint64_t count, uint32_t op, float scalar,
                               uint32_t period,
                               hipStream_t stream);

@@ -137,6 +137,19 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const float* a, const 
 // maximum subtracted before expf, the exponentials summed in double, and
 // every one multiplied by the float of 1 / sum. One block per row; out may
 // alias in (each element is read before it is written, by the same thread).
+// op_attn_temperature (S/graph/session.hpp:343-347): block i scales row i
+// by its position's temperature, each element one f32 multiply
+// (kernels::scale).
+__global__ __launch_bounds__(256) void temperature_kernel(const float* in, float* out, uint32_t size, uint32_t pos,
+                                                          uint32_t floor_len, float scale) {
+    const uint32_t i = blockIdx.x;
+    const float t = attn_temperature(pos + i, scale, floor_len);
+    const std::size_t base = static_cast<std::size_t>(i) * size;
+    for (uint32_t e = threadIdx.x; e < size; e += 256) {
+        out[base + e] = in[base + e] * t;
+    }
+}
+
 __global__ __launch_bounds__(256) void softmax_kernel(const float* in, float* out, uint32_t size) {
     __shared__ float wmax[4];
     __shared__ double wsum[4];
@@ -282,6 +295,12 @@ hipError_t launch_pixel_shuffle(const float* in, float* out, uint32_t n, uint32_
                                 hipStream_t stream) {
     const uint64_t count = uint64_t{grid_w} * grid_h * n;
     pixel_shuffle_kernel<<<grid_for(count), 256, 0, stream>>>(in, out, n, grid_w, s, count);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_temperature(const float* in, float* out, uint32_t n, uint32_t size, uint32_t pos,
+                                   uint32_t floor_len, float scale, hipStream_t stream) {
+    temperature_kernel<<<n, 256, 0, stream>>>(in, out, size, pos, floor_len, scale);
     return hipGetLastError();
 }
 

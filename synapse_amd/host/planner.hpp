@@ -59,9 +59,11 @@ constexpr std::size_t align_up(std::size_t n) noexcept {
     return (n + plan_alignment - 1) / plan_alignment * plan_alignment;
 }
 
-inline memory_plan plan(const compute_graph& g) {
+// The plan for given live intervals (at least liveness(g)'s): a caller that
+// runs some nodes' work later than the graph says extends its tensors'
+// intervals first.
+inline memory_plan plan(const compute_graph& g, const std::vector<live_interval>& live) {
     const auto& tensors = g.tensors();
-    const auto live = liveness(g);
     std::vector<tensor_id> order(tensors.size());
     std::iota(order.begin(), order.end(), tensor_id{0});
     std::stable_sort(order.begin(), order.end(),
@@ -92,9 +94,12 @@ inline memory_plan plan(const compute_graph& g) {
     return p;
 }
 
-inline bool plan_is_valid(const compute_graph& g, const memory_plan& p) {
+inline memory_plan plan(const compute_graph& g) {
+    return plan(g, liveness(g));
+}
+
+inline bool plan_is_valid(const compute_graph& g, const memory_plan& p, const std::vector<live_interval>& live) {
     const auto& tensors = g.tensors();
-    const auto live = liveness(g);
     if (p.offset.size() != tensors.size()) {
         return false;
     }
@@ -111,6 +116,10 @@ inline bool plan_is_valid(const compute_graph& g, const memory_plan& p) {
         }
     }
     return true;
+}
+
+inline bool plan_is_valid(const compute_graph& g, const memory_plan& p) {
+    return plan_is_valid(g, p, liveness(g));
 }
 
 }  // namespace syn::graph

@@ -16,6 +16,11 @@
 // Inputs are written and outputs read with write()/read(), the device
 // counterparts of tensor(t) (:107-110). A HIP failure during a run stops
 // it, returns false and is kept in status().
+//
+// One fusion: a layer's op_rope(q), op_rope(k), op_attn_temperature(q) and
+// op_attention run as one syn_hip_attention_rope call, which a decode step
+// makes one kernel (the RoPE and temperature nodes are skipped; the RoPE
+// inputs stay live in the memory plan up to the attention).
 #pragma once
 
 #include "graph.hpp"
@@ -23,6 +28,8 @@
 
 #include <array>
 #include <cmath>
+#include <limits>
+#include <optional>
 #include <span>
 #include <unordered_map>
 
@@ -38,9 +45,98 @@ struct batch {  // tokens.size() consecutive tokens, the first at pos
     std::uint32_t pos = 0;
 };
 
+// An op_attention whose q is op_rope's result (directly, or through
+// op_attn_temperature) and whose k is op_rope's result, with those results
+// read by nothing else and not graph outputs, both rotations alike and of
+// the cache's head size: the nodes folded into it.
+struct rope_fold {
+    static constexpr std::size_t none = ~std::size_t{0};
+    std::size_t rope_q = none;
+    std::size_t rope_k = none;
+    std::size_t temperature = none;
+};
+
+inline bool same_rotation(const op_rope& a, const op_rope& b) noexcept {
+    return a.head_dim == b.head_dim && a.theta_scale == b.theta_scale && a.mode == b.mode &&
+           a.freq_factors == b.freq_factors && a.scaling.freq_scale == b.scaling.freq_scale &&
+           a.scaling.ext_factor == b.scaling.ext_factor && a.scaling.attn_factor == b.scaling.attn_factor &&
+           a.scaling.corr_low == b.scaling.corr_low && a.scaling.corr_high == b.scaling.corr_high;
+}
+
+// Per node: its fold if it is such an attention.
+inline std::vector<std::optional<rope_fold>> find_rope_folds(const compute_graph& g) {
+    const auto& nodes = g.nodes();
+    const std::size_t n_t = g.tensors().size();
+    std::vector<std::size_t> producer(n_t, rope_fold::none);
+    std::vector<std::size_t> readers(n_t, 0);
+    for (std::size_t i = 0; i < nodes.size(); ++i) {
+        for (tensor_id t : results(nodes[i])) {
+            producer[t] = i;
+        }
+        for (tensor_id t : operands(nodes[i])) {
+            ++readers[t];
+        }
+    }
+    for (tensor_id t : g.outputs()) {
+        ++readers[t];  // an output is read by the caller
+    }
+    const auto only_for = [&](tensor_id t) { return t < n_t && readers[t] == 1 && producer[t] != rope_fold::none; };
+    std::vector<std::optional<rope_fold>> folds(nodes.size());
+    for (std::size_t i = 0; i < nodes.size(); ++i) {
+        const auto* a = std::get_if<op_attention>(&nodes[i]);
+        if (a == nullptr || !only_for(a->q) || !only_for(a->k)) {
+            continue;
+        }
+        rope_fold f;
+        std::size_t q_src = producer[a->q];
+        if (const auto* t = std::get_if<op_attn_temperature>(&nodes[q_src])) {
+            if (!only_for(t->in) || t->floor_len == 0 || t->floor_len > std::numeric_limits<std::uint32_t>::max()) {
+                continue;
+            }
+            f.temperature = q_src;
+            q_src = producer[t->in];
+        }
+        const auto* rq = std::get_if<op_rope>(&nodes[q_src]);
+        const auto* rk = std::get_if<op_rope>(&nodes[producer[a->k]]);
+        if (rq == nullptr || rk == nullptr || !same_rotation(*rq, *rk) ||
+            rq->head_dim != g.states()[a->cache].head_dim) {
+            continue;
+        }
+        f.rope_q = q_src;
+        f.rope_k = producer[a->k];
+        folds[i] = f;
+    }
+    return folds;
+}
+
+// liveness(g) with each folded RoPE input kept up to its attention.
+inline std::vector<live_interval> liveness_with_folds(const compute_graph& g,
+                                                      const std::vector<std::optional<rope_fold>>& folds) {
+    auto live = liveness(g);
+    for (std::size_t i = 0; i < folds.size(); ++i) {
+        if (folds[i]) {
+            for (std::size_t r : {folds[i]->rope_q, folds[i]->rope_k}) {
+                const tensor_id in = std::get<op_rope>(g.nodes()[r]).in;
+                live[in].last = std::max(live[in].last, i);
+            }
+        }
+    }
+    return live;
+}
+
 class session {
 public:
-    explicit session(const compute_graph& g) : graph_(&g), plan_(plan(g)) {
+    explicit session(const compute_graph& g)
+        : graph_(&g), folds_(find_rope_folds(g)), plan_(plan(g, liveness_with_folds(g, folds_))) {
+        folded_.assign(g.nodes().size(), false);
+        for (const auto& f : folds_) {
+            if (f) {
+                folded_[f->rope_q] = folded_[f->rope_k] = true;
+                if (f->temperature != rope_fold::none) {
+                    folded_[f->temperature] = true;
+                }
+            }
+        }
         // Run sizes go to the device as 32-bit counts.
         if (g.max_batch() > std::numeric_limits<std::uint32_t>::max()) {
             status_ = SYN_HIP_EUNSUPPORTED;
@@ -268,6 +364,9 @@ private:
     bool execute_all(std::size_t rows, std::size_t images, std::uint32_t pos) noexcept {
         const auto& nodes = graph_->nodes();
         for (std::size_t i = 0; i < nodes.size(); ++i) {
+            if (folded_[i]) {
+                continue;  // done by its attention's syn_hip_attention_rope
+            }
             const int e = std::visit([&](const auto& op) { return execute(op, i, rows, images, pos); }, nodes[i]);
             if (!keep(e)) {
                 return false;
@@ -364,18 +463,25 @@ private:
     // Each row times its position's temperature: a float quotient, the log
     // in double, rounded to float (kernels::attn_temperature,
     // S/kernels/elementwise.hpp:66-71).
+    // One launch per image; the device computes each row's factor from its
+    // position (syn_hip_attn_temperature).
     int execute(const op_attn_temperature& o, std::size_t, std::size_t rows, std::size_t images,
                 std::uint32_t pos) noexcept {
-        const std::uint64_t row = size_of(o.in) * sizeof(float);
+        if (o.floor_len == 0 || o.floor_len > std::numeric_limits<std::uint32_t>::max()) {
+            return SYN_HIP_EINVAL;
+        }
+        const std::uint64_t image = std::uint64_t{rows} * size_of(o.in) * sizeof(float);
         for (std::size_t img = 0; img < images; ++img) {
-            for (std::size_t r = 0; r < rows; ++r) {
-                const float q = std::floor(static_cast<float>(pos + r) / static_cast<float>(o.floor_len));
-                const auto t = static_cast<float>(std::log(static_cast<double>(q) + 1.0) * o.scale + 1.0);
-                const std::uint64_t at = (img * rows + r) * row;
-                if (const int e = elementwise(SYN_SCALE, plan_.offset[o.in] + at, no_offset, plan_.offset[o.out] + at,
-                                              size_of(o.in), t)) {
-                    return e;
-                }
+            syn_temperature_desc d{};
+            d.in_offset = plan_.offset[o.in] + img * image;
+            d.out_offset = plan_.offset[o.out] + img * image;
+            d.n = static_cast<std::uint32_t>(rows);
+            d.size = static_cast<std::uint32_t>(size_of(o.in));
+            d.pos = pos;
+            d.floor_len = static_cast<std::uint32_t>(o.floor_len);
+            d.scale = o.scale;
+            if (const int e = syn_hip_attn_temperature(arena_, &d)) {
+                return e;
             }
         }
         return SYN_HIP_OK;
@@ -432,7 +538,7 @@ private:
         return SYN_HIP_OK;
     }
 
-    int execute(const op_attention& a, std::size_t, std::size_t rows, std::size_t, std::uint32_t pos) noexcept {
+    int execute(const op_attention& a, std::size_t i, std::size_t rows, std::size_t, std::uint32_t pos) noexcept {
         syn_attn_desc d{};
         d.cache = kv_[a.cache];
         d.q_offset = plan_.offset[a.q];
@@ -447,7 +553,31 @@ private:
         d.scale = a.scale;
         d.q_dtype = SYN_F32;
         d.kv_dtype = SYN_F32;
-        return syn_hip_attention(arena_, &d);
+        if (!folds_[i]) {
+            return syn_hip_attention(arena_, &d);
+        }
+        const rope_fold& f = *folds_[i];
+        const auto& rq = std::get<op_rope>(graph_->nodes()[f.rope_q]);
+        const auto& rk = std::get<op_rope>(graph_->nodes()[f.rope_k]);
+        syn_attn_rope_desc r{};
+        d.q_offset = plan_.offset[rq.in];
+        d.k_offset = plan_.offset[rk.in];
+        r.q_out_offset = plan_.offset[a.q];
+        r.k_out_offset = plan_.offset[a.k];
+        r.freq_factors_offset = const_offset_[f.rope_q];
+        r.theta_scale = rq.theta_scale;
+        r.mode = rq.mode == rope_mode::neox ? 1u : 0u;
+        r.freq_scale = rq.scaling.freq_scale;
+        r.ext_factor = rq.scaling.ext_factor;
+        r.attn_factor = rq.scaling.attn_factor;
+        r.corr_low = rq.scaling.corr_low;
+        r.corr_high = rq.scaling.corr_high;
+        if (f.temperature != rope_fold::none) {
+            const auto& t = std::get<op_attn_temperature>(graph_->nodes()[f.temperature]);
+            r.temp_scale = t.scale;
+            r.temp_floor_len = static_cast<std::uint32_t>(t.floor_len);
+        }
+        return syn_hip_attention_rope(arena_, &d, &r);
     }
 
     int execute(const op_self_attention& s, std::size_t, std::size_t rows, std::size_t images,
@@ -468,6 +598,8 @@ private:
     }
 
     const compute_graph* graph_;
+    std::vector<std::optional<rope_fold>> folds_;  // per node: the RoPE folded into this attention
+    std::vector<bool> folded_;                     // per node: run inside a later attention
     memory_plan plan_;
     std::vector<std::uint64_t> const_offset_;                  // per node: its RoPE table, or ~0
     std::vector<std::array<std::uint64_t, 2>> weight_offset_;  // per node: its bound matrices

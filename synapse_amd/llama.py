@@ -30,8 +30,8 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import capi
-from .capi import (NO_OFFSET, SYN_ADD, SYN_F32, SYN_SCALE, SYN_SILU_MUL, Arena, AttnDesc, ElementwiseDesc, EmbedDesc,
-                   MatmulDesc, MatmulQDesc, NormDesc, RopeDesc, check, lib)
+from .capi import (NO_OFFSET, SYN_ADD, SYN_F32, SYN_SILU_MUL, Arena, AttnDesc, AttnRopeDesc, ElementwiseDesc, EmbedDesc,
+                   MatmulDesc, MatmulQDesc, NormDesc, check, lib)
 from .gguf import F32, Q4_0, Q4_K, Q5_0, Q6_K, Q8_0, TYPE_NAMES, GGUFError, GGUFFile
 
 _f32 = np.float32
@@ -305,14 +305,21 @@ class DeviceLlama:
                             count=count, op=op, scalar=scalar)
         check(lib().syn_hip_elementwise(self.arena.handle, ctypes.byref(d)))
 
-    def _rope(self, x, out, size, pos):
+    def _attention(self, layer, pos):
+        """op_rope on q and k, op_attn_temperature, op_attention: one
+        syn_hip_attention_rope call, which a decode step runs as one kernel."""
         c, s = self.config, self.config.rope_scaling
-        d = RopeDesc(in_offset=self.act[x], out_offset=self.act[out],
-                     freq_factors_offset=self.off[self.freq_factors] if self.freq_factors else NO_OFFSET, n=1,
-                     size=size, head_dim=c.head_dim, pos=pos, theta_scale=self.theta_scale, mode=c.rope_mode,
-                     freq_scale=s.freq_scale, ext_factor=s.ext_factor, attn_factor=s.attn_factor,
-                     corr_low=s.corr_low, corr_high=s.corr_high)
-        check(lib().syn_hip_rope(self.arena.handle, ctypes.byref(d)))
+        ad = AttnDesc(cache=self.caches[layer], q_offset=self.act["q"], k_offset=self.act["k"],
+                      v_offset=self.act["v"], out_offset=self.act["attn"], scratch_offset=self.scratch[0],
+                      scratch_bytes=self.scratch[1], n_heads=c.n_head, pos=pos, n=1, scale=self.scale,
+                      q_dtype=SYN_F32, kv_dtype=SYN_F32)
+        rd = AttnRopeDesc(q_out_offset=self.act["qr"], k_out_offset=self.act["kr"],
+                          freq_factors_offset=self.off[self.freq_factors] if self.freq_factors else NO_OFFSET,
+                          theta_scale=self.theta_scale, mode=c.rope_mode, freq_scale=s.freq_scale,
+                          ext_factor=s.ext_factor, attn_factor=s.attn_factor, corr_low=s.corr_low,
+                          corr_high=s.corr_high, temp_scale=c.attn_temp_scale,
+                          temp_floor_len=c.n_ctx_orig if c.attn_temp_scale != 0.0 else 0)
+        check(lib().syn_hip_attention_rope(self.arena.handle, ctypes.byref(ad), ctypes.byref(rd)))
 
     def step(self, token: int, pos: int) -> np.ndarray:
         c = self.config
@@ -330,16 +337,7 @@ class DeviceLlama:
             self._matmul(b + "attn_q.weight", "h", "q", q_rows, E, b + "attn_q.bias")
             self._matmul(b + "attn_k.weight", "h", "k", kv_rows, E, b + "attn_k.bias")
             self._matmul(b + "attn_v.weight", "h", "v", kv_rows, E, b + "attn_v.bias")
-            self._rope("q", "qr", q_rows, pos)
-            self._rope("k", "kr", kv_rows, pos)
-            if c.attn_temp_scale != 0.0:  # after RoPE, as llm_build_mistral3
-                t = attn_temperature(pos, c.attn_temp_scale, c.n_ctx_orig)
-                self._elementwise(SYN_SCALE, "qr", None, "qr", q_rows, t)
-            ad = AttnDesc(cache=self.caches[l], q_offset=self.act["qr"], k_offset=self.act["kr"],
-                          v_offset=self.act["v"], out_offset=self.act["attn"], scratch_offset=self.scratch[0],
-                          scratch_bytes=self.scratch[1], n_heads=c.n_head, pos=pos, n=1, scale=self.scale,
-                          q_dtype=SYN_F32, kv_dtype=SYN_F32)
-            check(lib().syn_hip_attention(self.arena.handle, ctypes.byref(ad)))
+            self._attention(l, pos)  # RoPE, then the temperature after it (llm_build_mistral3), then attention
             self._matmul(b + "attn_output.weight", "attn", "o", E, q_rows, b + "attn_output.bias")
             self._elementwise(SYN_ADD, "o", "x", "x", E)
             self._norm("x", b + "ffn_norm.weight", "h")

@@ -12,6 +12,8 @@ struct syn_arena {
 
 namespace stub {
 long calls = 0;  // device work the session asked for
+// Calls by entry point, for the launch counts of a decode layer.
+long rope = 0, temperature = 0, attention = 0, attention_rope = 0;
 }
 
 namespace {
@@ -46,9 +48,23 @@ uint64_t syn_hip_attention_scratch_bytes(uint32_t n_heads, uint32_t n_kv, uint32
     return n_kv == 0 || n_heads % n_kv ? 0 : align256(uint64_t{(max_ctx + 127) / 128} * n_heads * (hd + 2) * 4);
 }
 uint64_t syn_hip_matmul_q_act_bytes(uint32_t, uint32_t n, uint32_t cols) { return uint64_t{n} * cols + 1024; }
-int syn_hip_attention(syn_arena*, const syn_attn_desc*) { return ok(); }
+int syn_hip_attention(syn_arena*, const syn_attn_desc*) {
+    ++stub::attention;
+    return ok();
+}
+int syn_hip_attention_rope(syn_arena*, const syn_attn_desc*, const syn_attn_rope_desc*) {
+    ++stub::attention_rope;
+    return ok();
+}
+int syn_hip_attn_temperature(syn_arena*, const syn_temperature_desc*) {
+    ++stub::temperature;
+    return ok();
+}
 int syn_hip_self_attention(syn_arena*, const syn_self_desc*) { return ok(); }
-int syn_hip_rope(syn_arena*, const syn_rope_desc*) { return ok(); }
+int syn_hip_rope(syn_arena*, const syn_rope_desc*) {
+    ++stub::rope;
+    return ok();
+}
 int syn_hip_embed(syn_arena*, const syn_embed_desc*, const uint32_t*, uint32_t) { return ok(); }
 int syn_hip_rms_norm(syn_arena*, const syn_norm_desc*) { return ok(); }
 int syn_hip_matmul(syn_arena*, const syn_matmul_desc*) { return ok(); }

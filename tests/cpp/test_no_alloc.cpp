@@ -9,12 +9,14 @@
 #include "graph.hpp"
 #include "session.hpp"
 
+#include <cstdio>
 #include <cstdlib>
 #include <new>
 #include <vector>
 
 namespace stub {
 extern long calls;
+extern long rope, temperature, attention, attention_rope;
 }
 
 namespace {
@@ -123,6 +125,37 @@ void llama_runs() {
     CHECK(ran);
     CHECK(allocations == 0);
     CHECK(stub::calls - before > 13 * 20);  // the runs did ask for device work
+
+    // A decode step's layer: RoPE of q and k, the temperature and the
+    // attention fold into one syn_hip_attention_rope call (one kernel on the
+    // device) -- 1 call per layer where the graph has 4 nodes.
+    const long rope0 = stub::rope, temp0 = stub::temperature, attn0 = stub::attention, fused0 = stub::attention_rope;
+    const long calls0 = stub::calls;
+    CHECK(s.run(step{5, 24}));
+    CHECK(stub::attention_rope - fused0 == 2);
+    CHECK(stub::rope == rope0 && stub::temperature == temp0 && stub::attention == attn0);
+    const long per_step = stub::calls - calls0;
+
+    // The same graph with q's rotation also read elsewhere cannot fold: the
+    // separate calls, the temperature one launch per run.
+    graph_builder b2(n_batch);
+    tensor_id h2 = b2.embed(table.ref());
+    const tensor_id x2 = b2.rms_norm(h2, norm.ref(), 1e-5f);
+    const tensor_id qr = b2.rope(b2.matmul(wq.ref(), x2), hd, 1e4f);
+    const tensor_id q2 = b2.attn_temperature(qr, 0.1f, 8);
+    const tensor_id k2 = b2.rope(b2.matmul(wk.ref(), x2), hd, 1e4f);
+    const tensor_id a2 = b2.attention(q2, k2, b2.matmul(wv.ref(), x2), b2.kv_cache(ctx, kv_heads, hd), heads, 0.25f);
+    b2.output(b2.add(b2.matmul(wo.ref(), a2), qr));
+    auto g2 = std::move(b2).finalize();
+    CHECK(g2.has_value());
+    if (g2) {
+        session s2{g2.value()};
+        const long r1 = stub::rope, t1 = stub::temperature, a1 = stub::attention, f1 = stub::attention_rope;
+        CHECK(s2.run(batch{std::span<const std::uint32_t>(tokens, 6), 0}));
+        CHECK(stub::rope - r1 == 2 && stub::temperature - t1 == 1 && stub::attention - a1 == 1);
+        CHECK(stub::attention_rope == f1);
+    }
+    std::printf("decode step: %ld C-ABI calls for 2 layers\n", per_step);
 }
 
 // An image encoder (S/models/clip.hpp:300-417): layer norm, projection,

@@ -1,0 +1,151 @@
+"""GPU: RoPE and the attention temperature folded into the attention call.
+
+syn_hip_attention_rope runs a layer's op_rope(q), op_rope(k),
+op_attn_temperature(q) and op_attention (S/graph/session.hpp:337-374) as
+one call; a single-token step is one decode kernel that rotates q and the new
+K row in LDS. It is checked bit for bit against the separate calls
+(syn_hip_rope, syn_hip_attn_temperature, syn_hip_attention) on identical
+caches: outputs and every cache row. The runs it does not fuse (several
+tokens, head sizes the split-KV kernel does not take) make the separate calls
+themselves and must write the rotated rows where the descriptor says.
+syn_hip_attn_temperature is checked against the reference's formula
+(S/kernels/elementwise.hpp:66-72) evaluated on the host.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from gpu_util import SYN_F32, Arena, attn_desc, capi, check, lib, put_rows, scratch_for
+from synapse_amd import workloads as wl
+from synapse_amd.capi import AttnRopeDesc, RopeDesc, TemperatureDesc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def arena():
+    a = Arena(1 << 30)
+    yield a
+    a.close()
+
+
+def _host_temperature(pos: np.ndarray, scale: float, floor_len: int) -> np.ndarray:
+    q = np.floor(pos.astype(np.float32) / np.float32(floor_len)).astype(np.float32)
+    return (np.log(q.astype(np.float64) + 1.0) * np.float64(np.float32(scale)) + 1.0).astype(np.float32)
+
+
+def _rope_params(hd, mode, yarn, ff_off):
+    sc = [0.25, 1.0, 0.9, 8.0, 23.0] if yarn else [1.0, 0.0, 1.0, 0.0, 0.0]
+    theta_scale = float(np.float32(500000.0) ** np.float32(-2.0 / hd))
+    return dict(freq_factors_offset=ff_off, theta_scale=theta_scale, mode=mode, freq_scale=sc[0],
+                ext_factor=sc[1], attn_factor=sc[2], corr_low=sc[3], corr_high=sc[4])
+
+
+def _layer(arena, n_heads, n_kv, hd, ctx, n, mode=0, yarn=False, ff=False, temp=None, seed=1):
+    """Runs one layer both ways on two caches holding the same ctx rows;
+    returns (fused out, separate out, fused cache, separate cache, rotated
+    q and k rows the fused call wrote)."""
+    g = wl.rng(seed)
+    row, qsz = n_kv * hd, n_heads * hd
+    kc = wl.to_f16_bits(wl.normal(g, (ctx, row))) if ctx else None
+    vc = wl.to_f16_bits(wl.normal(g, (ctx, row))) if ctx else None
+    q, k, v = wl.normal(g, (n, qsz)), wl.normal(g, (n, row)), wl.normal(g, (n, row))
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    mark = arena.top
+    caches = [capi.kv_state(arena, ctx + n, n_kv, hd) for _ in range(2)]
+    if ctx:
+        for c in caches:
+            capi.upload_cache(arena, c, kc, vc)
+    ff_off = put_rows(arena, (1.0 + np.arange(hd // 2) % 4).astype(np.float32), SYN_F32) if ff else capi.NO_OFFSET
+    p = _rope_params(hd, mode, yarn, ff_off)
+    q_off, k_off, v_off = (put_rows(arena, x, SYN_F32) for x in (q, k, v))
+    qr_off, kr_off = arena.alloc(q.nbytes), arena.alloc(k.nbytes)
+    outs = [arena.alloc(n * qsz * 4) for _ in range(2)]
+    scratch = scratch_for(arena, n_heads, n_kv, hd, ctx + n)
+    # Separate calls: rope q, [temperature], rope k, attention.
+    for src, dst, size in ((q_off, qr_off, qsz), (k_off, kr_off, row)):
+        d = RopeDesc(in_offset=src, out_offset=dst, n=n, size=size, head_dim=hd, pos=ctx, **p)
+        check(lib().syn_hip_rope(arena.handle, ctypes.byref(d)))
+        if temp is not None and src == q_off:
+            t = TemperatureDesc(in_offset=qr_off, out_offset=qr_off, n=n, size=qsz, pos=ctx, floor_len=temp[1],
+                                scale=temp[0])
+            check(lib().syn_hip_attn_temperature(arena.handle, ctypes.byref(t)))
+    d = attn_desc(caches[1], qr_off, kr_off, v_off, outs[1], scratch, n_heads, ctx, n, scale)
+    check(lib().syn_hip_attention(arena.handle, ctypes.byref(d)))
+    want_qr = arena.download(qr_off, q.shape, np.float32)
+    want_kr = arena.download(kr_off, k.shape, np.float32)
+    # Fused: the unrotated rows in, rotated rows (if any) to fresh buffers.
+    qr2, kr2 = arena.alloc(q.nbytes), arena.alloc(k.nbytes)
+    check(lib().syn_hip_fill(arena.handle, qr2, 0, q.nbytes))
+    check(lib().syn_hip_fill(arena.handle, kr2, 0, k.nbytes))
+    d = attn_desc(caches[0], q_off, k_off, v_off, outs[0], scratch, n_heads, ctx, n, scale)
+    r = AttnRopeDesc(q_out_offset=qr2, k_out_offset=kr2, temp_scale=temp[0] if temp else 0.0,
+                     temp_floor_len=temp[1] if temp else 0, **p)
+    check(lib().syn_hip_attention_rope(arena.handle, ctypes.byref(d), ctypes.byref(r)))
+    got = [arena.download(o, (n, qsz), np.float32) for o in outs]
+    cache_rows = [capi.download_cache(arena, c, ctx + n) for c in caches]
+    rotated = (arena.download(qr2, q.shape, np.float32), arena.download(kr2, k.shape, np.float32))
+    arena.top = mark
+    return got[0], got[1], cache_rows[0], cache_rows[1], rotated, (want_qr, want_kr)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,ctx,mode,yarn,ff,temp", [
+    (32, 8, 128, 4096, 0, False, False, None),        # config 2 with Llama RoPE
+    (32, 8, 128, 4096, 0, False, True, None),         # with frequency factors (Llama 3.1)
+    (28, 4, 128, 1000, 1, False, False, None),        # neox pairs (Qwen2)
+    (32, 8, 128, 300, 0, True, False, (0.5, 8192)),   # YaRN and the temperature (Mistral 3)
+    (4, 2, 16, 15, 0, False, False, (0.1, 8)),        # the tiny models' shape, whole-softmax length
+    (8, 4, 64, 0, 1, True, True, (0.1, 1)),           # first position
+    (16, 1, 256, 2047, 0, False, False, None),
+])
+def test_decode_step_fused_equals_separate_calls(arena, n_heads, n_kv, hd, ctx, mode, yarn, ff, temp):
+    got, want, cache_f, cache_s, rotated, _ = _layer(arena, n_heads, n_kv, hd, ctx, 1, mode, yarn, ff, temp,
+                                                     seed=ctx + hd)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(cache_f[0], cache_s[0]) and np.array_equal(cache_f[1], cache_s[1])
+    # One kernel: the rotated rows never leave the chip.
+    assert not rotated[0].any() and not rotated[1].any()
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,ctx,n", [(32, 8, 128, 100, 37), (4, 2, 12, 20, 1), (6, 2, 20, 0, 5)])
+def test_unfused_runs_make_the_separate_calls(arena, n_heads, n_kv, hd, ctx, n):
+    """Several tokens (prefill) and head sizes the split-KV kernel does not
+    take: the same results, and the rotated rows where the descriptor says."""
+    got, want, cache_f, cache_s, rotated, want_rot = _layer(arena, n_heads, n_kv, hd, ctx, n, 0, False, True,
+                                                            (0.25, 4), seed=n + hd)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(cache_f[0], cache_s[0]) and np.array_equal(cache_f[1], cache_s[1])
+    assert np.array_equal(rotated[0], want_rot[0]) and np.array_equal(rotated[1], want_rot[1])
+
+
+def test_fused_step_rejects_f16_rows(arena):
+    hd, n_heads, n_kv = 64, 4, 2
+    mark = arena.top
+    cache = capi.kv_state(arena, 8, n_kv, hd)
+    buf = arena.alloc(1 << 16)
+    d = attn_desc(cache, buf, buf, buf, buf + 4096, (buf, 0), n_heads, 0, 1, 0.125, q_dtype=capi.SYN_F16)
+    r = AttnRopeDesc(q_out_offset=buf, k_out_offset=buf, **_rope_params(hd, 0, False, capi.NO_OFFSET))
+    assert lib().syn_hip_attention_rope(arena.handle, ctypes.byref(d), ctypes.byref(r)) == -1  # SYN_HIP_EINVAL
+    arena.top = mark
+
+
+@pytest.mark.parametrize("pos,n,floor_len,scale", [(0, 4096, 8192, 0.1), (8190, 300, 8192, 0.1), (0, 2048, 1, 0.5),
+                                                   (123456, 100, 4, 0.25), (4294967000, 200, 7, 0.3)])
+def test_attn_temperature_matches_the_reference_formula(arena, pos, n, floor_len, scale):
+    """One launch for n rows; each row's factor computed on the device equals
+    the reference's float quotient, double logarithm, float rounding."""
+    size = 64
+    x = wl.normal(wl.rng(pos % 1000 + n), (n, size))
+    mark = arena.top
+    off = put_rows(arena, x, SYN_F32)
+    out = arena.alloc(x.nbytes)
+    d = TemperatureDesc(in_offset=off, out_offset=out, n=n, size=size, pos=pos, floor_len=floor_len, scale=scale)
+    check(lib().syn_hip_attn_temperature(arena.handle, ctypes.byref(d)))
+    got = arena.download(out, x.shape, np.float32)
+    arena.top = mark
+    t = _host_temperature(np.arange(pos, pos + n, dtype=np.uint64).astype(np.uint32), scale, floor_len)
+    want = (x * t[:, None]).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

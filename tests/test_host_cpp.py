@@ -75,6 +75,12 @@ def test_graph_builder_and_planner():
     _run("test_graph")
 
 
+def test_rope_sin_cos_correctly_rounded():
+    """The RoPE kernels' own sin and cos (Cody-Waite and Taylor series in
+    double), built for the host: correctly rounded for angles up to 2^32."""
+    _run("test_rope_math")
+
+
 def test_session_run_allocates_nothing():
     """session::run under a counting operator new, against a C ABI that
     launches nothing (tests/sdk/graph_no_alloc.cpp:199-263 restated)."""

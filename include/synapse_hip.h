@@ -207,6 +207,7 @@ typedef struct syn_rope_desc {
     float theta_scale;            /* base^(-2/head_dim) */
     uint32_t mode;                /* 0 normal, 1 neox */
     float freq_scale, ext_factor, attn_factor, corr_low, corr_high;
+    uint32_t period;              /* rows per image: row i at pos + i % period (images restart); 0: pos + i */
 } syn_rope_desc;
 
 int syn_hip_rope(syn_arena* arena, const syn_rope_desc* desc);

@@ -44,7 +44,7 @@ class SelfDesc(ctypes.Structure):
 class RopeDesc(ctypes.Structure):
     _fields_ = [("in_offset", u64), ("out_offset", u64), ("freq_factors_offset", u64), ("n", u32), ("size", u32),
                 ("head_dim", u32), ("pos", u32), ("theta_scale", f32), ("mode", u32), ("freq_scale", f32),
-                ("ext_factor", f32), ("attn_factor", f32), ("corr_low", f32), ("corr_high", f32)]
+                ("ext_factor", f32), ("attn_factor", f32), ("corr_low", f32), ("corr_high", f32), ("period", u32)]
 
 
 class AttnRopeDesc(ctypes.Structure):

@@ -932,6 +932,7 @@ int syn_hip_rope(syn_arena* a, const syn_rope_desc* d) {
     r.attn_factor = d->attn_factor;
     r.corr_low = d->corr_low;
     r.corr_high = d->corr_high;
+    r.period = d->period;
     return hip_status(syn::launch_rope(r, a->stream), "rope launch");
 }
 

@@ -246,6 +246,7 @@ struct rope_args {
     const float* freq_factors;  // or nullptr
     uint32_t n, size, hd, pos, mode;
     float theta_scale, freq_scale, ext_factor, attn_factor, corr_low, corr_high;
+    uint32_t period;  // rows per image (positions restart), or 0
 };
 hipError_t launch_rope(const rope_args& a, hipStream_t stream);
 

@@ -20,7 +20,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const rope_args a) {
     const uint32_t half = a.hd / 2;
     if (threadIdx.x < 64) {
         float th0, th1;
-        rope_thetas(a.pos + i, a.theta_scale, half, threadIdx.x, th0, th1);
+        rope_thetas(a.pos + (a.period != 0 ? i % a.period : i), a.theta_scale, half, threadIdx.x, th0, th1);
         rope_table(a, th0, th1, half, a.freq_factors, tab, threadIdx.x);
     }
     __syncthreads();

@@ -491,16 +491,15 @@ private:
         return syn_hip_copy(arena_, plan_.offset[o.out], plan_.offset[o.in] + (rows * images - 1) * row, row);
     }
     // Table row i added to row i of each image (rows start again per image).
+    // One launch for every image: the table's rows*size floats repeat over
+    // the images (SYN_ADD_BIAS with the image as its period).
     int execute(const op_add_rows& o, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t) noexcept {
         const std::uint64_t image = std::uint64_t{rows} * size_of(o.in);
-        for (std::size_t img = 0; img < images; ++img) {
-            if (const int e = elementwise(SYN_ADD, plan_.offset[o.in] + img * image * sizeof(float),
-                                          weight_offset_[i][0], plan_.offset[o.out] + img * image * sizeof(float),
-                                          image)) {
-                return e;
-            }
+        if (image > std::numeric_limits<std::uint32_t>::max()) {
+            return SYN_HIP_EUNSUPPORTED;
         }
-        return SYN_HIP_OK;
+        return elementwise(SYN_ADD_BIAS, plan_.offset[o.in], weight_offset_[i][0], plan_.offset[o.out],
+                           image * images, 0.0f, static_cast<std::uint32_t>(image));
     }
     int execute(const op_pixel_shuffle& o, std::size_t, std::size_t rows, std::size_t, std::uint32_t) noexcept {
         syn_pixel_shuffle_desc d{};
@@ -513,29 +512,25 @@ private:
         return syn_hip_pixel_shuffle(arena_, &d);
     }
 
+    // One launch for every image, positions restarting per image.
     int execute(const op_rope& r, std::size_t i, std::size_t rows, std::size_t images, std::uint32_t pos) noexcept {
-        const std::size_t size = graph_->tensors()[r.in].size;
-        for (std::size_t img = 0; img < images; ++img) {
-            syn_rope_desc d{};
-            d.in_offset = plan_.offset[r.in] + img * rows * size * sizeof(float);
-            d.out_offset = plan_.offset[r.out] + img * rows * size * sizeof(float);
-            d.freq_factors_offset = const_offset_[i];
-            d.n = static_cast<std::uint32_t>(rows);
-            d.size = static_cast<std::uint32_t>(size);
-            d.head_dim = static_cast<std::uint32_t>(r.head_dim);
-            d.pos = pos;
-            d.theta_scale = r.theta_scale;
-            d.mode = r.mode == rope_mode::neox ? 1u : 0u;
-            d.freq_scale = r.scaling.freq_scale;
-            d.ext_factor = r.scaling.ext_factor;
-            d.attn_factor = r.scaling.attn_factor;
-            d.corr_low = r.scaling.corr_low;
-            d.corr_high = r.scaling.corr_high;
-            if (const int e = syn_hip_rope(arena_, &d)) {
-                return e;
-            }
-        }
-        return SYN_HIP_OK;
+        syn_rope_desc d{};
+        d.in_offset = plan_.offset[r.in];
+        d.out_offset = plan_.offset[r.out];
+        d.freq_factors_offset = const_offset_[i];
+        d.n = static_cast<std::uint32_t>(rows * images);
+        d.period = static_cast<std::uint32_t>(rows);
+        d.size = static_cast<std::uint32_t>(graph_->tensors()[r.in].size);
+        d.head_dim = static_cast<std::uint32_t>(r.head_dim);
+        d.pos = pos;
+        d.theta_scale = r.theta_scale;
+        d.mode = r.mode == rope_mode::neox ? 1u : 0u;
+        d.freq_scale = r.scaling.freq_scale;
+        d.ext_factor = r.scaling.ext_factor;
+        d.attn_factor = r.scaling.attn_factor;
+        d.corr_low = r.scaling.corr_low;
+        d.corr_high = r.scaling.corr_high;
+        return syn_hip_rope(arena_, &d);
     }
 
     int execute(const op_attention& a, std::size_t i, std::size_t rows, std::size_t, std::uint32_t pos) noexcept {

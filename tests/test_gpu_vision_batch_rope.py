@@ -185,6 +185,58 @@ def test_rope_position_zero_is_identity(arena):
     assert np.array_equal(arena.download(out_off, x.shape, np.float32), x)
 
 
+def _rope_desc(in_off, out_off, n, size, hd, pos, period=0, mode=0):
+    return capi.RopeDesc(in_offset=in_off, out_offset=out_off, freq_factors_offset=capi.NO_OFFSET, n=n, size=size,
+                         head_dim=hd, pos=pos, theta_scale=orc.rope_theta_scale(5e5, hd), mode=mode, freq_scale=1.0,
+                         ext_factor=0.0, attn_factor=1.0, corr_low=0.0, corr_high=0.0, period=period)
+
+
+def test_rope_period_restarts_positions_per_image(arena):
+    """Several images in one launch (period = rows per image): each image's
+    rows are rotated at pos, pos + 1, ... as separate per-image calls do."""
+    rows, images, hd, size = 5, 3, 64, 256
+    x = wl.normal(wl.rng(8), (rows * images, size))
+    mark = arena.top
+    in_off = put_rows(arena, x, SYN_F32)
+    one, each = arena.alloc(x.nbytes), arena.alloc(x.nbytes)
+    check(lib().syn_hip_rope(arena.handle, ctypes.byref(_rope_desc(in_off, one, rows * images, size, hd, 7, rows))))
+    for img in range(images):
+        at = img * rows * size * 4
+        check(lib().syn_hip_rope(arena.handle, ctypes.byref(_rope_desc(in_off + at, each + at, rows, size, hd, 7))))
+    got, want = arena.download(one, x.shape, np.float32), arena.download(each, x.shape, np.float32)
+    arena.top = mark
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_rope_cos_sin_are_correctly_rounded(arena):
+    """Rotating (1, 0) pairs returns each pair's (cos, sin): the angle is the
+    f32 chain pos * theta_scale^p, and cos and sin of it are the correctly
+    rounded f32 values (float64 on the host), for positions up to 2^31."""
+    hd = 128
+    pos = np.array([0, 1, 4095, 4096, 131071, 2**24 + 1, 2**31 - 5], dtype=np.uint32)
+    x = np.tile(np.array([1.0, 0.0], np.float32), hd // 2)[None, :]
+    mark = arena.top
+    in_off = put_rows(arena, x, SYN_F32)
+    out = arena.alloc(x.nbytes)
+    ts = np.float32(orc.rope_theta_scale(5e5, hd))
+    wrong = 0
+    for p in pos:
+        check(lib().syn_hip_rope(arena.handle, ctypes.byref(_rope_desc(in_off, out, 1, hd, hd, int(p)))))
+        got = arena.download(out, x.shape, np.float32)[0]
+        theta = np.empty(hd // 2, np.float32)
+        th = np.float32(p)
+        for i in range(hd // 2):
+            theta[i] = th
+            th = np.float32(th * ts)
+        cs = np.cos(theta.astype(np.float64)).astype(np.float32)
+        sn = np.sin(theta.astype(np.float64)).astype(np.float32)
+        wrong += int(np.sum(got[0::2] != cs) + np.sum(got[1::2] != sn))
+        assert np.all(np.abs(got[0::2] - cs) <= np.spacing(np.abs(cs))) and \
+            np.all(np.abs(got[1::2] - sn) <= np.spacing(np.abs(sn)))
+    arena.top = mark
+    assert wrong <= 1, wrong  # float64 then float32 may round a rare tie twice
+
+
 # ---- descriptor checks (nothing is launched) ------------------------------------
 
 def test_bad_descriptors_are_errors_not_faults(arena):

@@ -42,7 +42,7 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
 # HBM bytes one config-2 decode step moves (split + merge kernels), from two
 # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a copy of known
 # size; profiles/decode_c2_pmc_traffic.md has the runs and the factors.
-DECODE_TRAFFIC_BYTES = 18_253_056
+DECODE_TRAFFIC_BYTES = 18_254_080
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 matrix, TFLOP/s
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 matrix, TOP/s
 
@@ -135,17 +135,17 @@ def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int,
     graph_ms, reps = None, 0
     if graph:
         byref = [ctypes.byref(d) for d in descs]
-        hg = capi.HipGraph(arena, lambda: [check(L.syn_hip_attention(arena.handle, r)) for r in byref])
         reps = max(1, steps // layers)
-        for _ in range(2):
-            hg.launch()
-        arena.sync()
-        hip.record(t0, stream)
-        for _ in range(reps):
-            hg.launch()
-        hip.record(t1, stream)
-        graph_ms = hip.ms(t0, t1) / (reps * layers)
-        hg.close()
+        with capi.HipGraph(arena, lambda: [check(L.syn_hip_attention(arena.handle, r)) for r in byref]) as hg:
+            for _ in range(2):
+                hg.launch()
+            arena.sync()
+            hip.record(t0, stream)
+            for _ in range(reps):
+                hg.launch()
+            hip.record(t1, stream)
+            graph_ms = hip.ms(t0, t1) / (reps * layers)
+            arena.sync()
         out_g = arena.download(descs[0].out_offset, (qsz,), np.float32)
         assert np.array_equal(out_g.view(np.uint32), out.view(np.uint32))
     arena.close()

@@ -199,9 +199,21 @@ class HipGraph:
         _hip_ok(self._rt.hipGraphLaunch(self._exec, self.stream), "hipGraphLaunch")
 
     def close(self) -> None:
+        """Destroys the executable graph; the caller has synchronised every
+        launch of it. Before the arena is closed, on every path: a graph
+        left alive is otherwise torn down with the runtime at process exit."""
         if self._exec:
             self._rt.hipGraphExecDestroy(self._exec)
             self._exec = ctypes.c_void_p()
+
+    def __enter__(self) -> "HipGraph":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
+
+    def __del__(self):
+        self.close()
 
 
 _rt = None

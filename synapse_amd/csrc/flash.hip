@@ -509,14 +509,12 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
     }
 }
 
+// f16 rows only: f32 rows of images this short take the f32 kernel
+// (generic.hip), which keeps the reference's f32 arithmetic.
 template <int HD>
-hipError_t launch_resident(const flash_args& a, uint32_t dtype, uint32_t lds_bytes, hipStream_t stream) {
+hipError_t launch_resident(const flash_args& a, uint32_t lds_bytes, hipStream_t stream) {
     const dim3 grid(a.n_heads * a.batch);
-    if (dtype == 1) {
-        resident_kernel<HD, true><<<grid, 256, lds_bytes, stream>>>(a);
-    } else {
-        resident_kernel<HD, false><<<grid, 256, lds_bytes, stream>>>(a);
-    }
+    resident_kernel<HD, true><<<grid, 256, lds_bytes, stream>>>(a);
     return hipGetLastError();
 }
 
@@ -537,19 +535,19 @@ hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStrea
     const uint32_t hdp = (a.hd + 31) / 32 * 32;
     // Resident form while two blocks fit a CU's LDS (160 KB).
     // (An image's rows are addressed through one buffer resource: < 2^31 bytes.)
-    if (hdp <= 128 && uint64_t{a.n_heads} * a.batch <= 0x7fffffffu &&
-        uint64_t{a.n} * a.row * (in_dtype == 1 ? 2 : 4) < (uint64_t{1} << 31)) {
+    if (in_dtype == 1 && hdp <= 128 && uint64_t{a.n_heads} * a.batch <= 0x7fffffffu &&
+        uint64_t{a.n} * a.row * 2 < (uint64_t{1} << 31)) {
         const uint32_t bytes = resident_lds_bytes(a.n, hdp);
         if (bytes <= resident_lds_limit) {
             switch (hdp) {
             case 32:
-                return launch_resident<32>(a, in_dtype, bytes, stream);
+                return launch_resident<32>(a, bytes, stream);
             case 64:
-                return launch_resident<64>(a, in_dtype, bytes, stream);
+                return launch_resident<64>(a, bytes, stream);
             case 96:
-                return launch_resident<96>(a, in_dtype, bytes, stream);
+                return launch_resident<96>(a, bytes, stream);
             default:
-                return launch_resident<128>(a, in_dtype, bytes, stream);
+                return launch_resident<128>(a, bytes, stream);
             }
         }
     }

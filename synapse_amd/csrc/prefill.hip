@@ -582,7 +582,9 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
     };
 
     // One 64-key tile from one LDS stage (the 4-wave kernel's step).
-    const auto compute = [&](uint32_t t0, const char* sk, const char* sv) __attribute__((always_inline)) {
+    // W: this item may hold queries that take their softmax whole (the first
+    // key tile of the first query tile); only the group's first item can.
+    const auto compute = [&]<bool W>(uint32_t t0, const char* sk, const char* sv) __attribute__((always_inline)) {
         if (q_row0 >= a.n || t0 > wave_last_pos) {
             return;
         }
@@ -635,7 +637,18 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
         }
         const float mc = (m_run == -INFINITY ? 0.0f : m_run) * c;
         h8 pv[4];
-        const bool whole = probabilities(t0, a.pos + q_row0, my_pos, mc, sc, pv, c);
+        bool whole = false;
+        if constexpr (W) {
+            whole = probabilities(t0, a.pos + q_row0, my_pos, mc, sc, pv, c);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    pv[2 * e + (i >> 3)][i & 7] = to_h(fast_exp2(sc[e][i] * c - mc));
+                }
+            }
+        }
         float psum = 0.0f;
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2) {
@@ -682,7 +695,7 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
             enter(qt);
             cur_qt = qt;
         }
-        compute(item_kt(j) * pf_bk, sk, sv);
+        compute.template operator()<false>(item_kt(j) * pf_bk, sk, sv);
     };
     // The group's pipeline over its items; both groups take `half` steps
     // (two barriers each), so every barrier has all 8 waves.
@@ -700,8 +713,13 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
             tail(0, v0);
         }
         pf_barrier();
+        // Item 0 apart, the only one that can hold whole-softmax queries, so
+        // the loop's items keep the plain form's registers. The loop is the
+        // same sequence rotated: each item, then its two barriers.
+        if (cnt > 0) {
+            compute.template operator()<true>(item_kt(0) * pf_bk, k0, v0);
+        }
         for (uint32_t j = 0; j < half; j += 2) {
-            run(j, k0, v0);
             pf_barrier();
             if (j + 2 < cnt) {
                 issue(j + 2, k0, v0);
@@ -724,6 +742,10 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
                 tail(j + 2, v0);
             }
             pf_barrier();
+            if (j + 2 >= half) {
+                break;
+            }
+            run(j + 2, k0, v0);
         }
     };
     reset();

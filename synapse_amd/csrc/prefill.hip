@@ -596,10 +596,20 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
                 sc[e][i] = 0.0f;
             }
             const char* krow = sk + ((32 * e + pf_slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
+            // The slice's K operands read in one batch ahead of its products
+            // (left to itself, the scheduler reused one register and waited
+            // out each read's latency before its product).
+            h8 kop[NS];
 #pragma unroll
             for (int st = 0; st < NS; ++st) {
-                sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
+                kop[st] = *reinterpret_cast<const h8*>(krow + 16 * st);
             }
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                sc[e] = mfma32(kop[st], qv[st], sc[e]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, NS, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
         }
         if (t0 + pf_bk - 1 > a.pos + q_row0 || t0 + pf_bk > kv_end) {
             const uint32_t lim = max(min(my_pos + 1, kv_end), t0) - t0;

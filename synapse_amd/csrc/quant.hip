@@ -13,6 +13,9 @@
 
 #include "quant.hpp"
 
+#include <atomic>
+#include <mutex>
+
 namespace syn {
 
 namespace {
@@ -438,6 +441,48 @@ uint32_t matmul_q_rows_per_pass(uint32_t n, uint32_t cols) {
     return 0;
 }
 
+namespace {
+
+// Per-device launch facts for the GEMV, asked of the runtime once: the CU
+// count, and the resident workgroups per CU of each (kernel, LDS size). A
+// small fixed table (no allocation); past its end the runtime is asked each call.
+constexpr int gemv_max_devices = 64;
+std::atomic<int> gemv_cus[gemv_max_devices];
+
+struct gemv_occupancy {
+    std::atomic<const void*> kernel{nullptr};
+    std::atomic<uint32_t> lds{0};
+    std::atomic<int> per_cu{0};
+};
+constexpr int gemv_occupancy_slots = 64;
+gemv_occupancy gemv_occupancy_table[gemv_max_devices][gemv_occupancy_slots];
+
+// The slot of (kernel, lds) on dev, claimed if new; null when the row is full.
+gemv_occupancy* gemv_occupancy_of(int dev, const void* kernel, uint32_t lds) {
+    static std::mutex claim;
+    auto& row = gemv_occupancy_table[dev];
+    for (auto& e : row) {
+        if (e.kernel.load(std::memory_order_acquire) == kernel && e.lds.load(std::memory_order_relaxed) == lds) {
+            return &e;
+        }
+    }
+    std::lock_guard<std::mutex> lock(claim);
+    for (auto& e : row) {
+        const void* k = e.kernel.load(std::memory_order_relaxed);
+        if (k == kernel && e.lds.load(std::memory_order_relaxed) == lds) {
+            return &e;
+        }
+        if (k == nullptr) {
+            e.lds.store(lds, std::memory_order_relaxed);
+            e.kernel.store(kernel, std::memory_order_release);
+            return &e;
+        }
+    }
+    return nullptr;
+}
+
+}  // namespace
+
 hipError_t launch_matmul_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
                            uint32_t n, uint32_t rows, uint32_t cols, hipStream_t stream) {
     if (n >= matmul_q_gemm_rows) {
@@ -448,20 +493,36 @@ hipError_t launch_matmul_q(uint32_t t, const uint8_t* w, const float* x, uint8_t
         return hipErrorInvalidValue;
     }
     const uint32_t lds = gemv_lds_bytes(nr, cols / 32);
-    int dev = 0, cus = 0;
+    int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) {
         return e;
     }
-    if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev); e != hipSuccess) {
-        return e;
+    if (dev < 0 || dev >= gemv_max_devices) {
+        return hipErrorInvalidDevice;
+    }
+    // The device's CU count, asked once per device.
+    int cus = gemv_cus[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev); e != hipSuccess) {
+            return e;
+        }
+        gemv_cus[dev].store(cus, std::memory_order_relaxed);
     }
     const auto go = [&]<uint32_t T>() {
         const auto run = [&](auto kernel) {
             // A resident grid: as many 8-wave workgroups as the CUs hold at
-            // once with this kernel's registers and this LDS.
-            int per_cu = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 512, lds) != hipSuccess || per_cu < 1) {
-                per_cu = 1;
+            // once with this kernel's registers and this LDS. The occupancy
+            // query runs once per (device, kernel, LDS size) and is kept.
+            gemv_occupancy* slot = gemv_occupancy_of(dev, reinterpret_cast<const void*>(kernel), lds);
+            int per_cu = slot ? slot->per_cu.load(std::memory_order_relaxed) : 0;
+            if (per_cu < 1) {
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 512, lds) != hipSuccess ||
+                    per_cu < 1) {
+                    per_cu = 1;
+                }
+                if (slot) {
+                    slot->per_cu.store(per_cu, std::memory_order_relaxed);
+                }
             }
             const uint32_t resident = static_cast<uint32_t>(cus) * static_cast<uint32_t>(per_cu);
             const dim3 grid(std::min((rows + 7) / 8, resident), (n + nr - 1) / nr);

@@ -233,165 +233,170 @@ __global__ __launch_bounds__(256) void flash_kernel(const flash_args a) {
 }
 
 // ---- head-resident form -------------------------------------------------------
-// When an image's K and V^T for one head fit in LDS (short rows, as a ViT's
-// 257 tokens), a block owns one (image, head): it stages all n keys once --
-// K rows padded by one 16-byte chunk, V transposed to V^T rows -- and then
-// its waves sweep their 32-query tiles over the resident keys in 32-key
-// slices, with no further barriers or global loads besides q. Keys past n
-// are zero rows and masked.
+// When one head of one image (a unit: its K rows and V^T) fits in half a
+// CU's LDS (short rows, as a ViT's 257 tokens), a block of 4 waves keeps it
+// resident, two blocks per CU. Every load of the block goes out at the
+// start (K rows, V rows and each wave's q tiles, into registers); the K rows
+// then go to padded LDS rows and V is transposed to V^T rows, and after one
+// barrier wave w0 sweeps query tiles w0, w0 + 4, ... over the unit's keys in
+// 32-key slices, with no further barriers or K/V loads. Keys past n are zero
+// rows and masked.
 
-// LDS bytes of the resident form for n keys (keys padded to a multiple of 32).
+// LDS bytes of one unit's K rows and V^T for n keys (padded to 32).
 __host__ __device__ constexpr uint32_t resident_lds_bytes(uint32_t n, uint32_t hdp) {
     const uint32_t np = (n + 31) / 32 * 32;
     return np * (hdp / 8 + 1) * 16 + hdp * (np / 8 + 1) * 16;
+}
+// A last query tile of at most this many rows that would be a third tile on
+// one wave (query tiles = 1 mod 4, as 257 rows make 9) is computed on the
+// vector units instead, by that wave, after its tiles, so every wave sweeps
+// the same number of tiles. Its LDS: the rows' q and one probability row.
+constexpr uint32_t resident_tail_rows = 2;
+__host__ __device__ constexpr uint32_t resident_tail_bytes(uint32_t n, uint32_t hdp) {
+    return resident_tail_rows * hdp * 2 + (n + 31) / 32 * 32 * 4;
+}
+__host__ __device__ constexpr bool resident_has_tail(uint32_t n) {
+    const uint32_t n_qt = (n + 31) / 32;
+    return n_qt % 4 == 1 && n - 32 * (n_qt - 1) <= resident_tail_rows;
+}
+__host__ __device__ constexpr uint32_t resident_unit_bytes(uint32_t n, uint32_t hdp) {
+    return resident_lds_bytes(n, hdp) + (resident_has_tail(n) ? resident_tail_bytes(n, hdp) : 0u);
 }
 // Two blocks per CU: at most 80 KB each.
 constexpr uint32_t resident_lds_limit = 80 * 1024;
 // The most keys (a multiple of 32) the resident form holds at head size hdp.
 __host__ __device__ constexpr uint32_t resident_max_keys(uint32_t hdp) {
     uint32_t np = 32;
-    while (resident_lds_bytes(np + 32, hdp) <= resident_lds_limit) {
+    while (resident_lds_bytes(np + 32, hdp) + resident_tail_bytes(np + 32, hdp) <= resident_lds_limit) {
         np += 32;
     }
     return np;
 }
-// Keys of the first staging half for np (padded) keys: about half, a
-// multiple of 64 (the compute steps' size), all of them up to 64.
-__host__ __device__ constexpr uint32_t resident_half1(uint32_t np) {
-    return np <= 64 ? np : (np / 128 > 0 ? np / 128 * 64 : 64);
-}
-// The most keys either half holds for up to npmax keys.
-__host__ __device__ constexpr uint32_t resident_half1_max(uint32_t npmax) {
-    uint32_t m = 0;
-    for (uint32_t np = 32; np <= npmax; np += 32) {
-        m = resident_half1(np) > m ? resident_half1(np) : m;
-    }
-    return m;
-}
-__host__ __device__ constexpr uint32_t resident_half2_max(uint32_t npmax) {
-    uint32_t m = 0;
-    for (uint32_t np = 32; np <= npmax; np += 32) {
-        m = np - resident_half1(np) > m ? np - resident_half1(np) : m;
-    }
-    return m;
-}
 
-template <int HD, bool F16>
+template <int HD>
 __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
     constexpr int NS = HD / 16;      // k-steps of the score product
     constexpr int NT = HD / 32;      // 32-dim tiles of the output
     constexpr int KCPR = HD / 8;     // 16-byte chunks of a K row
     constexpr int KROWC = KCPR + 1;  // LDS K row in chunks (one of padding)
+    constexpr uint32_t WAVES = 4;
+    constexpr uint32_t THREADS = 64 * WAVES;
+    constexpr uint32_t NPMAX = resident_max_keys(HD);
+    constexpr uint32_t KC = (NPMAX * KCPR + THREADS - 1) / THREADS;      // K chunks per thread and unit
+    constexpr uint32_t VC = (NPMAX / 2 * KCPR + THREADS - 1) / THREADS;  // V key pairs per thread and unit
+    constexpr uint32_t QT = (NPMAX / 32 + WAVES - 1) / WAVES;  // q tiles per wave, at most
     extern __shared__ __attribute__((aligned(16))) char lds[];
 
     const int tid = threadIdx.x;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ln = tid & 63;
     const int H = ln >> 5;
     const int qi = ln & 31;
+    // Wave w0 takes tiles w0, w0 + WAVES, ...; rotated by the block so that
+    // the extra tiles of co-resident blocks land on different SIMDs.
+    const uint32_t w0 = (static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(tid >> 6)) + blockIdx.x) % WAVES;
     const uint32_t n = a.n;
     const uint32_t hd = a.hd;
     const uint32_t np = (n + 31) / 32 * 32;
     const uint32_t vrowc = np / 8 + 1;  // LDS V^T row in chunks (one of padding)
-    const uint32_t h = blockIdx.x % a.n_heads;
-    const uint32_t img = blockIdx.x / a.n_heads;
-    const std::size_t row_base = static_cast<std::size_t>(img) * n;
-    const float c = a.scale_log2e;
-    char* lk = lds;
-    char* lv = lds + np * KROWC * 16;
-
-    // ---- stage K rows and V^T in two halves of the keys ----
-    // Keys [0, kh) are the first half and [kh, np) the second. Every load of
-    // the block is issued at once, q and the first half first; the waves then
-    // run all their query tiles over the first half while the second half
-    // lands, and finish over the second. Zeros past n and past hd.
-    // f32 rows take twice the staging registers: they stage all keys at
-    // once (the first half is everything).
-    constexpr uint32_t NPMAX = resident_max_keys(HD);
-    constexpr uint32_t CH1 = ((F16 ? resident_half1_max(NPMAX) : NPMAX) * KCPR + 255) / 256;  // chunks per thread
-    constexpr uint32_t CH2 = F16 ? (resident_half2_max(NPMAX) * KCPR + 255) / 256 : 1;
-    constexpr uint32_t ESZ = F16 ? 2 : 4;
-    const uint32_t kh = F16 ? resident_half1(np) : np;
-    // The image's rows through buffer resources: chunks past n or past hd
-    // take an out-of-range offset and read as zeros, so every load is
-    // unconditional.
-    const uint32_t img_bytes = n * a.row * ESZ;
-    const rsrc k_res = make_rsrc(static_cast<const char*>(a.k_rows) + row_base * a.row * ESZ, img_bytes);
-    const rsrc v_res = make_rsrc(static_cast<const char*>(a.v_rows) + row_base * a.row * ESZ, img_bytes);
-    const auto chunk = [&](rsrc r, uint32_t off) {
-        if constexpr (F16) {
-            return buffer_load16(r, off);
-        } else {
-            const f4 lo = __builtin_bit_cast(f4, buffer_load16(r, off));
-            const f4 hi = __builtin_bit_cast(f4, buffer_load16(r, off == buffer_oob ? off : off + 16));
-            return as_u4(h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]), to_h(hi[0]), to_h(hi[1]),
-                            to_h(hi[2]), to_h(hi[3])});
-        }
-    };
-    // The wave's q tiles (wave (w + block) % 4 takes tiles w', w' + 4, ..., so
-    // the extra tiles of co-resident blocks land on different SIMDs) go out
-    // first.
-    constexpr uint32_t TPW = (NPMAX / 32 + 3) / 4;  // q tiles per wave, at most
     const uint32_t n_qt = np / 32;
-    const uint32_t w0 = (static_cast<uint32_t>(w) + blockIdx.x) % 4;
-    const rsrc q_res = make_rsrc(static_cast<const char*>(a.q) + row_base * a.q_row * ESZ, n * a.q_row * ESZ);
-    u4 qc[TPW][NS];
-#pragma unroll
-    for (uint32_t t = 0; t < TPW; ++t) {
-        const uint32_t my_q = 32 * (w0 + 4 * t) + qi;
-#pragma unroll
-        for (int st = 0; st < NS; ++st) {
-            const uint32_t d0 = H * (HD / 2) + 8 * st;
-            qc[t][st] = chunk(q_res, my_q < n && d0 < hd ? (my_q * a.q_row + h * hd + d0) * ESZ : buffer_oob);
-        }
-    }
-    // Chunk i of a half [k0, k1): K takes row-major chunks (consecutive lanes
-    // read consecutive 16 bytes of a row), V takes consecutive keys of one
-    // 8-dim chunk (each of the 8 half-word writes of a wave then covers 128
-    // contiguous bytes of a V^T row).
-    const auto load_half = [&]<uint32_t C>(uint32_t k0, uint32_t k1, u4 (&kc)[C], u4 (&vc)[C])
-                               __attribute__((always_inline)) {
-        const uint32_t count = (k1 - k0) * KCPR, span = max(k1 - k0, 1u);  // an empty half loads nothing
-#pragma unroll
-        for (uint32_t i = 0; i < C; ++i) {
-            const uint32_t idx = tid + 256 * i;
-            const uint32_t key = k0 + idx / KCPR, cc = idx % KCPR;
-            kc[i] = chunk(k_res, idx < count && key < n && 8 * cc < hd ? (key * a.row + h * hd + 8 * cc) * ESZ
-                                                                       : buffer_oob);
-            const uint32_t vkey = k0 + idx % span, vcc = idx / span;
-            vc[i] = chunk(v_res, idx < count && vkey < n && 8 * vcc < hd
-                                     ? (vkey * a.row + h * hd + 8 * vcc) * ESZ
-                                     : buffer_oob);
-        }
+    const bool tail = resident_has_tail(n);
+    const uint32_t n_mq = tail ? n_qt - 1 : n_qt;  // tiles on the matrix cores
+    const float c = a.scale_log2e;
+
+    // The unit's head, rows and LDS; its rows through buffer resources:
+    // chunks past n or past hd take an out-of-range offset and read as
+    // zeros, so every load is unconditional.
+    struct unit {
+        uint32_t h;
+        std::size_t row_base;
+        char* lk;
+        char* lv;
+        rsrc k_res, v_res, q_res;
     };
-    const auto store_half = [&]<uint32_t C>(uint32_t k0, uint32_t k1, const u4 (&kc)[C], const u4 (&vc)[C])
-                                __attribute__((always_inline)) {
-        const uint32_t count = (k1 - k0) * KCPR, span = max(k1 - k0, 1u);
+    unit U;
+    U.h = blockIdx.x % a.n_heads;
+    U.row_base = static_cast<std::size_t>(blockIdx.x / a.n_heads) * n;
+    U.lk = lds;
+    U.lv = lds + np * KROWC * 16;
+    const uint32_t img_bytes = n * a.row * 2;
+    U.k_res = make_rsrc(static_cast<const _Float16*>(a.k_rows) + U.row_base * a.row, img_bytes);
+    U.v_res = make_rsrc(static_cast<const _Float16*>(a.v_rows) + U.row_base * a.row, img_bytes);
+    U.q_res = make_rsrc(static_cast<const _Float16*>(a.q) + U.row_base * a.q_row, n * a.q_row * 2);
+
+    // Staging. K: chunk idx is chunk idx % KCPR of key idx / KCPR
+    // (consecutive lanes read consecutive 16 bytes of a row). V: the same
+    // over key pairs, a lane reading one 8-dim chunk of two consecutive
+    // keys, so each of its 8 dword writes to LDS puts one dim of both keys
+    // into a V^T row.
+    const auto load_unit = [&](u4 (&kc)[KC], u4 (&vc)[VC][2], u4 (&qc)[QT][NS], u4& tq)
+                               __attribute__((always_inline)) {
+        const uint32_t count = np * KCPR;
 #pragma unroll
-        for (uint32_t i = 0; i < C; ++i) {
-            const uint32_t idx = tid + 256 * i;
+        for (uint32_t i = 0; i < KC; ++i) {
+            const uint32_t idx = tid + THREADS * i;
+            const uint32_t key = idx / KCPR, cc = idx % KCPR;
+            kc[i] = buffer_load16(U.k_res, idx < count && key < n && 8 * cc < hd ? (key * a.row + U.h * hd + 8 * cc) * 2
+                                                                               : buffer_oob);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < VC; ++i) {
+            const uint32_t idx = tid + THREADS * i;
+            const uint32_t key = 2 * (idx / KCPR), cc = idx % KCPR;
+            const bool in = 2 * idx < count && 8 * cc < hd;
+#pragma unroll
+            for (uint32_t e = 0; e < 2; ++e) {
+                vc[i][e] = buffer_load16(U.v_res, in && key + e < n ? ((key + e) * a.row + U.h * hd + 8 * cc) * 2
+                                                                    : buffer_oob);
+            }
+        }
+        // The wave's first QT query tiles (tile w0 + WAVES t): lane (qi, H)
+        // holds dims H * HD / 2 + 8 st of row 32 tile + qi, the score
+        // product's operand.
+#pragma unroll
+        for (uint32_t t = 0; t < QT; ++t) {
+            const uint32_t tile = w0 + WAVES * t;
+            const uint32_t my_q = 32 * tile + qi;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                const uint32_t d0 = H * (HD / 2) + 8 * st;
+                qc[t][st] = buffer_load16(U.q_res, tile < n_mq && my_q < n && d0 < hd
+                                                       ? (my_q * a.q_row + U.h * hd + d0) * 2
+                                                       : buffer_oob);
+            }
+        }
+        // The tail rows' q, chunk ln (row ln / KCPR), for the wave that
+        // computes them.
+        const uint32_t tr = 32 * n_mq + ln / KCPR, tc = ln % KCPR;
+        tq = buffer_load16(U.q_res, tail && tr < n && 8 * tc < hd ? (tr * a.q_row + U.h * hd + 8 * tc) * 2
+                                                                  : buffer_oob);
+    };
+    const auto store_unit = [&](const u4 (&kc)[KC], const u4 (&vc)[VC][2]) __attribute__((always_inline)) {
+        const uint32_t count = np * KCPR;
+#pragma unroll
+        for (uint32_t i = 0; i < KC; ++i) {
+            const uint32_t idx = tid + THREADS * i;
             if (idx < count) {
-                const uint32_t key = k0 + idx / KCPR, cc = idx % KCPR;
-                *reinterpret_cast<u4*>(lk + (key * KROWC + cc) * 16) = kc[i];
-                const uint32_t vkey = k0 + idx % span, vcc = idx / span;
-                const h8 hv = as_h8(vc[i]);
-                _Float16* col = reinterpret_cast<_Float16*>(lv) + (8 * vcc * vrowc * 8 + vkey);
+                *reinterpret_cast<u4*>(U.lk + ((idx / KCPR) * KROWC + idx % KCPR) * 16) = kc[i];
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < VC; ++i) {
+            const uint32_t idx = tid + THREADS * i;
+            if (2 * idx < count) {
+                // The key count np is even, so a key pair is a dword of
+                // every V^T row.
+                const uint32_t key = 2 * (idx / KCPR), cc = idx % KCPR;
+                const h8 v0 = as_h8(vc[i][0]), v1 = as_h8(vc[i][1]);
+                _Float16* col = reinterpret_cast<_Float16*>(U.lv) + (8 * cc * vrowc * 8 + key);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    col[j * vrowc * 8] = hv[j];
+                    *reinterpret_cast<h2*>(col + j * vrowc * 8) = h2{v0[j], v1[j]};
                 }
             }
         }
     };
-    u4 kc1[CH1], vc1[CH1], kc2[CH2], vc2[CH2];
-    load_half(0, kh, kc1, vc1);
-    if constexpr (F16) {
-        load_half(kh, np, kc2, vc2);
-    }
 
-    // ---- the wave's query tiles over the resident keys ----
-    // The first tile runs over the first half while the second half lands;
-    // the other tiles start once all keys are resident.
+    // ---- a wave's query tiles over a unit's resident keys ----
     f16v o[NT];
     float m_run = -INFINITY, l_run = 0.0f;
     h8 qv[NS];
@@ -404,7 +409,7 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
             for (int i = 0; i < 16; ++i) {
                 sc[e][i] = 0.0f;
             }
-            const char* krow = lk + ((t0 + 32 * e + slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
+            const char* krow = U.lk + ((t0 + 32 * e + slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
 #pragma unroll
             for (int st = 0; st < NS; ++st) {
                 sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
@@ -428,93 +433,197 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             // V^T row 32t + qi, keys t0 + 8H + 16 s ..
-            const char* vrow = lv + ((32 * t + qi) * vrowc + t0 / 8 + H) * 16;
+            const char* vrow = U.lv + ((32 * t + qi) * vrowc + t0 / 8 + H) * 16;
 #pragma unroll
             for (int s2 = 0; s2 < 2 * E; ++s2) {
                 o[t] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[t]);
             }
         }
     };
-    // Keys [k0, k1) of the current tile (k0 a multiple of 64).
-    const auto sweep = [&](uint32_t k0, uint32_t k1) __attribute__((always_inline)) {
-        uint32_t t0 = k0;
-        for (; t0 + 64 <= k1; t0 += 64) {
-            step.template operator()<2>(t0);
-        }
-        if (t0 < k1) {
-            step.template operator()<1>(t0);
-        }
-    };
-    const auto begin_tile = [&](uint32_t tq) __attribute__((always_inline)) {
+    const auto run_unit = [&](const u4 (&qc)[QT][NS]) __attribute__((always_inline)) {
+        for (uint32_t t = 0; w0 + WAVES * t < n_mq; ++t) {
+            const uint32_t tq = w0 + WAVES * t;
+            const uint32_t my_q = 32 * tq + qi;
+            // The first QT tiles' q came with the staging; later ones load here.
+            if (t < QT) {
 #pragma unroll
-        for (int st = 0; st < NS; ++st) {
-            qv[st] = as_h8(qc[tq][st]);
-        }
+                for (uint32_t tt = 0; tt < QT; ++tt) {
+                    if (tt == t) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
+                        for (int st = 0; st < NS; ++st) {
+                            qv[st] = as_h8(qc[tt][st]);
+                        }
+                    }
+                }
+            } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                o[t][i] = 0.0f;
+                for (int st = 0; st < NS; ++st) {
+                    const uint32_t d0 = H * (HD / 2) + 8 * st;
+                    qv[st] = as_h8(buffer_load16(U.q_res, my_q < n && d0 < hd ? (my_q * a.q_row + U.h * hd + d0) * 2
+                                                                              : buffer_oob));
+                }
             }
-        }
-        m_run = -INFINITY;
-        l_run = 0.0f;
-    };
-    const auto end_tile = [&](uint32_t tq) __attribute__((always_inline)) {
-        const uint32_t my_q = 32 * (w0 + 4 * tq) + qi;
-        if (my_q >= n) {
-            return;
-        }
-        const float inv = 1.0f / l_run;
-        float* out = a.out + (row_base + my_q) * a.q_row + h * hd;
-        // Register i of tile t holds dim 32t + 8(i/4) + 4H + i%4.
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
+            for (int t = 0; t < NT; ++t) {
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const uint32_t d = 32 * t + 8 * b + 4 * H;
-                if (d < hd) {
-                    *reinterpret_cast<f4*>(out + d) =
-                        f4{o[t][4 * b] * inv, o[t][4 * b + 1] * inv, o[t][4 * b + 2] * inv, o[t][4 * b + 3] * inv};
+                for (int i = 0; i < 16; ++i) {
+                    o[t][i] = 0.0f;
+                }
+            }
+            m_run = -INFINITY;
+            l_run = 0.0f;
+            uint32_t t0 = 0;
+            for (; t0 + 64 <= np; t0 += 64) {
+                step.template operator()<2>(t0);
+            }
+            if (t0 < np) {
+                step.template operator()<1>(t0);
+            }
+            if (my_q < n) {
+                const float inv = 1.0f / l_run;
+                float* out = a.out + (U.row_base + my_q) * a.q_row + U.h * hd;
+                // Register i of tile t holds dim 32t + 8(i/4) + 4H + i%4.
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const uint32_t d = 32 * t + 8 * b + 4 * H;
+                        if (d < hd) {
+                            *reinterpret_cast<f4*>(out + d) = f4{o[t][4 * b] * inv, o[t][4 * b + 1] * inv,
+                                                                 o[t][4 * b + 2] * inv, o[t][4 * b + 3] * inv};
+                        }
+                    }
                 }
             }
         }
     };
-    // LDS-only barriers: the second half's loads stay in flight across the
-    // first. No wave still reads the first half's rows when another writes
-    // the second half's: the halves are disjoint in LDS.
-    const bool first = w0 < n_qt;  // this wave has a tile at all
-    store_half(0, kh, kc1, vc1);
-    lds_barrier();
-    if (first) {
-        begin_tile(0);
-        sweep(0, kh);
-    }
-    if constexpr (F16) {
-        store_half(kh, np, kc2, vc2);
-        lds_barrier();
-    }
-    if (first) {
-        sweep(kh, np);
-        end_tile(0);
-    }
-#pragma unroll
-    for (uint32_t tq = 1; tq < TPW; ++tq) {
-        if (w0 + 4 * tq >= n_qt) {
-            break;
+
+    // ---- the tail rows on the vector units ----
+    // Per row: lane l scores keys l, l + 64, ... (f32 sums of binary16
+    // products over the dims in order), the softmax is taken whole (max,
+    // sum, p = e / sum, kept in f32 in LDS), and lane d sums output dim d
+    // over the keys, 8 partial sums by key mod 8 added in order at the end.
+    const auto tail_rows = [&](u4 tq) __attribute__((always_inline)) {
+        const uint32_t r0 = 32 * n_mq;
+        const uint32_t rows = n - r0;
+        char* ltail = U.lv + HD * vrowc * 16;
+        _Float16* q_lds = reinterpret_cast<_Float16*>(ltail);                        // [tail rows][HD]
+        float* p_lds = reinterpret_cast<float*>(ltail + resident_tail_rows * HD * 2);  // [np]
+        if (static_cast<uint32_t>(ln) < rows * KCPR) {
+            *reinterpret_cast<u4*>(q_lds + (ln / KCPR) * HD + 8 * (ln % KCPR)) = tq;
         }
-        begin_tile(tq);
-        sweep(0, np);
-        end_tile(tq);
+        // Written and read by this wave only: its LDS operations complete in order.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        constexpr uint32_t KPL = (NPMAX + 63) / 64;  // keys per lane, at most
+        typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+        for (uint32_t i = 0; i < rows; ++i) {
+            h8 qr[KCPR];
+#pragma unroll
+            for (int ch = 0; ch < KCPR; ++ch) {
+                qr[ch] = *reinterpret_cast<const h8*>(q_lds + i * HD + 8 * ch);
+            }
+            // Chunk-major over the lane's keys, so each chunk's reads of all
+            // its keys are in flight together. Rows n..np-1 are zero rows;
+            // lanes past np read the last one.
+            float sj[KPL];
+#pragma unroll
+            for (uint32_t u = 0; u < KPL; ++u) {
+                sj[u] = 0.0f;
+            }
+#pragma unroll
+            for (int ch = 0; ch < KCPR; ++ch) {
+                h8 kk[KPL];
+#pragma unroll
+                for (uint32_t u = 0; u < KPL; ++u) {
+                    kk[u] = *reinterpret_cast<const h8*>(U.lk + (min(ln + 64 * u, np - 1) * KROWC + ch) * 16);
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < KPL; ++u) {
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        sj[u] = __builtin_amdgcn_fdot2(__builtin_bit_cast(fp16x2, h2{qr[ch][e], qr[ch][e + 1]}),
+                                                       __builtin_bit_cast(fp16x2, h2{kk[u][e], kk[u][e + 1]}), sj[u],
+                                                       false);
+                    }
+                }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (uint32_t u = 0; u < KPL; ++u) {
+                sj[u] = ln + 64 * u < n ? sj[u] : -INFINITY;
+                mx = fmaxf(mx, sj[u]);
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                mx = xor_max(mx, m);
+            }
+            float sum = 0.0f;
+#pragma unroll
+            for (uint32_t u = 0; u < KPL; ++u) {
+                sj[u] = fast_exp2((sj[u] - mx) * c);  // 0 past n
+                sum += sj[u];
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                sum = xor_sum(sum, m);
+            }
+            const float inv = 1.0f / sum;
+#pragma unroll
+            for (uint32_t u = 0; u < KPL; ++u) {
+                const uint32_t j = ln + 64 * u;
+                if (j < np) {
+                    p_lds[j] = sj[u] * inv;
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            float* out = a.out + (U.row_base + r0 + i) * a.q_row + U.h * hd;
+#pragma unroll
+            for (uint32_t d0 = 0; d0 < HD; d0 += 64) {
+                const uint32_t d = d0 + ln;
+                if (d < hd) {
+                    // V^T row d: keys 0..np-1 in order (zeros past n).
+                    const char* vrow = U.lv + d * vrowc * 16;
+                    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+                    for (uint32_t j8 = 0; j8 < np; j8 += 8) {
+                        const h8 vv = *reinterpret_cast<const h8*>(vrow + 2 * j8);
+                        const f4 p0 = *reinterpret_cast<const f4*>(p_lds + j8);
+                        const f4 p1 = *reinterpret_cast<const f4*>(p_lds + j8 + 4);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            acc[e] = fmaf(p0[e], static_cast<float>(vv[e]), acc[e]);
+                            acc[4 + e] = fmaf(p1[e], static_cast<float>(vv[4 + e]), acc[4 + e]);
+                        }
+                    }
+                    float r = acc[0];
+#pragma unroll
+                    for (int e = 1; e < 8; ++e) {
+                        r += acc[e];
+                    }
+                    out[d] = r;
+                }
+            }
+            // The next row rewrites p_lds: every lane's reads above are done.
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+    };
+
+    u4 kc[KC], vc[VC][2], qc[QT][NS], tq;
+    load_unit(kc, vc, qc, tq);
+    store_unit(kc, vc);
+    lds_barrier();
+    run_unit(qc);
+    if (tail && w0 == 0) {
+        tail_rows(tq);
     }
 }
 
 // f16 rows only: f32 rows of images this short take the f32 kernel
 // (generic.hip), which keeps the reference's f32 arithmetic.
 template <int HD>
-hipError_t launch_resident(const flash_args& a, uint32_t lds_bytes, hipStream_t stream) {
+hipError_t launch_resident(const flash_args& a, hipStream_t stream) {
     const dim3 grid(a.n_heads * a.batch);
-    resident_kernel<HD, true><<<grid, 256, lds_bytes, stream>>>(a);
+    resident_kernel<HD><<<grid, 256, resident_unit_bytes(a.n, HD), stream>>>(a);
     return hipGetLastError();
 }
 
@@ -537,17 +646,16 @@ hipError_t launch_bidirectional(const flash_args& a, uint32_t in_dtype, hipStrea
     // (An image's rows are addressed through one buffer resource: < 2^31 bytes.)
     if (in_dtype == 1 && hdp <= 128 && uint64_t{a.n_heads} * a.batch <= 0x7fffffffu &&
         uint64_t{a.n} * a.row * 2 < (uint64_t{1} << 31)) {
-        const uint32_t bytes = resident_lds_bytes(a.n, hdp);
-        if (bytes <= resident_lds_limit) {
+        if (resident_unit_bytes(a.n, hdp) <= resident_lds_limit) {
             switch (hdp) {
             case 32:
-                return launch_resident<32>(a, bytes, stream);
+                return launch_resident<32>(a, stream);
             case 64:
-                return launch_resident<64>(a, bytes, stream);
+                return launch_resident<64>(a, stream);
             case 96:
-                return launch_resident<96>(a, bytes, stream);
+                return launch_resident<96>(a, stream);
             default:
-                return launch_resident<128>(a, bytes, stream);
+                return launch_resident<128>(a, stream);
             }
         }
     }

@@ -250,6 +250,10 @@ struct rope_args {
 };
 hipError_t launch_rope(const rope_args& a, hipStream_t stream);
 
+// The current device's compute units, asked of the runtime once per device
+// (0 if the runtime cannot say).
+uint32_t device_cu_count();
+
 // ---- the rest of a decode graph (ops.hip) -----------------------------------
 constexpr uint32_t embed_max_tokens = 256;  // tokens per embed launch (kernel argument)
 struct embed_tokens {

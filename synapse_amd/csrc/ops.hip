@@ -10,6 +10,8 @@
 
 #include "kernels.hpp"
 
+#include <atomic>
+
 namespace syn {
 
 namespace {
@@ -259,6 +261,23 @@ uint32_t grid_for(uint64_t count) {
 }
 
 }  // namespace
+
+uint32_t device_cu_count() {
+    constexpr int max_devices = 64;
+    static std::atomic<int> cus[max_devices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= max_devices) {
+        return 0;
+    }
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) {
+            return 0;
+        }
+        cus[dev].store(v, std::memory_order_relaxed);
+    }
+    return static_cast<uint32_t>(v);
+}
 
 hipError_t launch_embed(const float* table, float* out, const embed_tokens& t, uint32_t n, uint32_t size,
                         hipStream_t stream) {

@@ -443,11 +443,10 @@ uint32_t matmul_q_rows_per_pass(uint32_t n, uint32_t cols) {
 
 namespace {
 
-// Per-device launch facts for the GEMV, asked of the runtime once: the CU
-// count, and the resident workgroups per CU of each (kernel, LDS size). A
-// small fixed table (no allocation); past its end the runtime is asked each call.
+// The resident workgroups per CU of each GEMV (kernel, LDS size) per device,
+// asked of the runtime once: a small fixed table (no allocation); past its
+// end the runtime is asked each call.
 constexpr int gemv_max_devices = 64;
-std::atomic<int> gemv_cus[gemv_max_devices];
 
 struct gemv_occupancy {
     std::atomic<const void*> kernel{nullptr};
@@ -500,13 +499,9 @@ hipError_t launch_matmul_q(uint32_t t, const uint8_t* w, const float* x, uint8_t
     if (dev < 0 || dev >= gemv_max_devices) {
         return hipErrorInvalidDevice;
     }
-    // The device's CU count, asked once per device.
-    int cus = gemv_cus[dev].load(std::memory_order_relaxed);
+    const uint32_t cus = device_cu_count();
     if (cus == 0) {
-        if (hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev); e != hipSuccess) {
-            return e;
-        }
-        gemv_cus[dev].store(cus, std::memory_order_relaxed);
+        return hipErrorInvalidDevice;
     }
     const auto go = [&]<uint32_t T>() {
         const auto run = [&](auto kernel) {
@@ -524,7 +519,7 @@ hipError_t launch_matmul_q(uint32_t t, const uint8_t* w, const float* x, uint8_t
                     slot->per_cu.store(per_cu, std::memory_order_relaxed);
                 }
             }
-            const uint32_t resident = static_cast<uint32_t>(cus) * static_cast<uint32_t>(per_cu);
+            const uint32_t resident = cus * static_cast<uint32_t>(per_cu);
             const dim3 grid(std::min((rows + 7) / 8, resident), (n + nr - 1) / nr);
             kernel<<<grid, 512, lds, stream>>>(w, x, act, bias, out, n, rows, cols);
         };

@@ -81,15 +81,54 @@ def test_vision_f32_beyond_lds_rows(arena):
 
 
 @pytest.mark.parametrize("n,hd", [(257, 64), (577, 64), (100, 128), (1, 64), (33, 32), (64, 64), (65, 64),
-                                  (96, 96), (190, 96), (128, 128), (288, 64), (540, 32)])
+                                  (96, 96), (190, 96), (128, 128), (288, 64), (540, 32), (258, 64), (2, 64),
+                                  (513, 32), (514, 32), (129, 96)])
 def test_vision_many_heads_f16(arena, n, hd):
     """Several images and heads at once with f16 inputs: every (image, head)
     block of the grid is checked. With keys resident, f16 rows are staged in
     two halves (the first query tile runs over the first while the second
     lands): the shapes cover no second half (n <= 64), a second half ending
     in a lone 32-key slice (65, 96, 257) and the largest resident n per head
-    size."""
+    size. A last query tile of one or two rows that would be a fifth tile of
+    32 (257, 258, 1, 2, 513, 514, 129 rows) is computed on the vector units."""
     _vision(arena, n, 3, 5, hd, SYN_F16, seed=11)
+
+
+def _tail_rows(arena, n, hd, batch, n_heads, images):
+    g = wl.rng(n + hd)
+    shape = (batch * n, n_heads * hd)
+    q, k, v = (wl.normal(g, shape, 0.5).astype(np.float16).astype(np.float32) for _ in range(3))
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    got = self_attention(arena, q, k, v, n, batch, n_heads, scale, SYN_F16)
+    tiles = (n + 31) // 32
+    first = 32 * (tiles - 1)
+    has_tail = tiles % 4 == 1 and n - first <= 2  # 4 waves per block
+    for b in images:
+        sl = slice(b * n, (b + 1) * n)
+        want = orc.self_attention(q[sl], k[sl], v[sl], n_heads, scale, threads=8)
+        assert_close(got[sl], want, what=f"image {b} n={n} heads={n_heads} hd={hd}")
+        if has_tail:
+            tail = np.abs(got[sl][first:] - want[first:]).max() / np.abs(want).max()
+            assert tail < 1e-5, (b, n, hd, tail)
+
+
+@pytest.mark.parametrize("n,hd", [(257, 64), (258, 64), (1, 64), (2, 64), (513, 32), (514, 32), (129, 96)])
+def test_vision_tail_rows_keep_f32_probabilities(arena, n, hd):
+    """The vector-unit rows (the last tile's one or two rows) keep p in f32
+    and sum in f32 over binary16-exact inputs, as the oracle does: within
+    1e-5 of the largest output, where the matrix-core rows (p rounded to
+    binary16) are held to the parity bound only. A wrong key, a dropped
+    key or a wrong head would miss by orders of magnitude. Few units: one
+    per 4-wave block, tail rows when the query tiles are 1 mod 4."""
+    _tail_rows(arena, n, hd, 2, 3, range(2))
+
+
+@pytest.mark.parametrize("n,hd", [(257, 64), (258, 64), (100, 64), (2, 64), (513, 32), (64, 32), (289, 32)])
+def test_vision_config5_grid(arena, n, hd):
+    """32 images x 16 heads: config 5's grid of 512 blocks, two per CU, at
+    other row counts (tail rows where the query tiles are 1 mod 4: 257, 258,
+    2, 513). Images 0, 15 and 31 are checked whole."""
+    _tail_rows(arena, n, hd, 32, 16, (0, 15, 31))
 
 
 @pytest.mark.parametrize("n,hd", [(13, 12), (50, 20), (6, 4)])

@@ -107,7 +107,8 @@ struct decode_traits<decode_batch_args> {
 // LDS of the split kernel: the group's q as given (f32 size, the larger),
 // the new K and V row of one head (likewise), per-wave (max, sum), the
 // waves' unscaled outputs (head rows padded by 4 floats), then a fused
-// step's RoPE table (hd/2 cos, hd/2 sin) and frequency factors (a 1 KB copy).
+// step's RoPE table (hd/2 cos, hd/2 sin), frequency factors (a 1 KB copy)
+// and the pairs' angles.
 inline __host__ __device__ uint32_t q_lds_bytes(uint32_t group, uint32_t hd) {
     return (group * hd * 4 + 15) / 16 * 16;
 }
@@ -118,7 +119,7 @@ inline __host__ __device__ uint32_t rope_lds_offset(uint32_t group, uint32_t hd)
     return q_lds_bytes(group, hd) + new_lds_bytes(hd) + (4 * 16 * 2 + 4 * group * (hd + 4)) * 4;
 }
 inline std::size_t decode_lds_bytes(uint32_t group, uint32_t hd) {
-    return rope_lds_offset(group, hd) + std::size_t{hd} * sizeof(float) + 1024;
+    return rope_lds_offset(group, hd) + std::size_t{hd} * sizeof(float) + 1024 + rope_max_pairs * sizeof(float);
 }
 
 // s_waitcnt immediate that waits until at most n vector memory operations
@@ -269,13 +270,13 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // (q also times the temperature factor), and the staging below reads the
     // rotated f32 rows as it reads unrotated ones.
     float* rope_tab = reinterpret_cast<float*>(lds_bytes + rope_lds_offset(group, hd));
-    float rope_th0 = 0.0f, rope_th1 = 0.0f;  // wave 0: the angles of pairs ln and ln + 64
     char* ff_lds = lds_bytes + rope_lds_offset(group, hd) + hd * 4;
+    float* rope_th = reinterpret_cast<float*>(ff_lds + 1024);  // the pairs' angles
     const auto rope_rows = [&]() {
         const uint32_t half = hd / 2;
         if (w == 0) {
             const float* ff = a_rope(a).freq_factors != nullptr ? reinterpret_cast<const float*>(ff_lds) : nullptr;
-            rope_table(a_rope(a), rope_th0, rope_th1, half, ff, rope_tab, static_cast<uint32_t>(ln));
+            rope_table(a_rope(a), rope_th, half, ff, rope_tab, static_cast<uint32_t>(ln));
         }
         lds_barrier();
         const bool normal = a_rope(a).mode == 0;
@@ -478,17 +479,22 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
             load16_lds(reinterpret_cast<const char*>(a.r.freq_factors) + off, ff_lds);
         }
     }
-    if (tb < t_end) {
+    // A fused RoPE step loads unconditionally: a wave with no positions
+    // reads past the resources' limits and gets zeros without memory
+    // traffic. (Guarded, the results met zero-initialised registers at the
+    // join, the compiler moved each as soon as it landed, waiting for it
+    // between the loads, and the angle chain below ran only after that.)
+    if (ROPE || tb < t_end) {
         load_kv(tb, kr, vr);
     }
     if constexpr (ROPE) {
-        // The angles need neither q nor the factors: wave 0 runs their
-        // chain while the loads are in flight.
-        if (w == 0) {
-            rope_thetas(new_t, a.r.theta_scale, hd / 2, static_cast<uint32_t>(ln), rope_th0, rope_th1);
+        // The angles need neither q nor the factors: lane 0 of wave 0 runs
+        // their chain while the loads are in flight.
+        if (w == 0 && ln == 0) {
+            rope_angles(new_t, a.r.theta_scale, hd / 2, rope_th);
         }
     }
-    convert_q(tb < t_end);
+    convert_q(ROPE || tb < t_end);
     float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));
     // A sequence of at most 128 rows is one split in which every wave takes
     // at most one step. Its softmax is then taken whole, as attend_group

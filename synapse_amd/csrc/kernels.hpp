@@ -102,27 +102,27 @@ hipError_t launch_decode(const decode_rope_args& a, uint32_t q_dtype, hipStream_
 
 constexpr uint32_t rope_max_pairs = 128;  // head_dim <= 256, as attention's
 
-// The angles of RoPE pairs p0 = lane and p1 = lane + 64 at position pos, as
-// rope() builds them (S/kernels/attention.hpp:101-127): pos times theta_scale
-// p times over by repeated f32 multiplication (not pow), so each angle is
-// the reference's to the last bit. Every lane runs the same chain over all
-// n_pairs (uniform control flow: a chain per lane of its own length was a
-// divergent loop that cost microseconds) and keeps the values at its pairs.
-__device__ inline void rope_thetas(uint32_t pos, float theta_scale, uint32_t n_pairs, uint32_t lane, float& t0,
-                                   float& t1) {
+// The angles of RoPE pairs 0 .. n_pairs-1 at position pos, as rope() builds
+// them (S/kernels/attention.hpp:101-127): pos times theta_scale p times over
+// by repeated f32 multiplication (not pow), so each angle is the reference's
+// to the last bit. One lane runs the chain and stores every angle to th (LDS)
+// as it goes: the chain is the only dependency. (Every lane running it and
+// keeping the values at its own pairs by compare and select per step cost
+// 1.9 us per fused decode step; a chain per lane of its own length was a
+// divergent loop.) The calling wave may read th right after: its LDS
+// operations complete in order.
+__device__ inline void rope_angles(uint32_t pos, float theta_scale, uint32_t n_pairs, float* th) {
 #pragma clang fp contract(off)
-    float th = static_cast<float>(pos);
-    t0 = th;
-    t1 = th;
+    float t = static_cast<float>(pos);
+    th[0] = t;
 #pragma unroll 8
     for (uint32_t j = 1; j < n_pairs; ++j) {
-        th *= theta_scale;
-        t0 = j == lane ? th : t0;
-        t1 = j == lane + 64 ? th : t1;
+        t *= theta_scale;
+        th[j] = t;
     }
 }
 
-// cos and sin of RoPE pair p with angle theta (rope_thetas), times the YaRN
+// cos and sin of RoPE pair p with angle theta (rope_angles), times the YaRN
 // magnitude, as rope() computes them (S/kernels/attention.hpp:101-121): every
 // product and sum rounds on its own; cos and sin of the f32 angle from
 // sincos_of. R has the fields of rope_params (theta_scale .. corr_high).
@@ -146,16 +146,16 @@ __device__ inline void rope_coeffs(const R& r, float theta, uint32_t p, float ff
 }
 
 // One wave builds the cos / sin table of every pair (n_pairs <= 128) into
-// tab[0 .. n_pairs) / tab[n_pairs .. 2 n_pairs) from the angles rope_thetas
-// gave its lanes; ff, if not null, holds the pairs' frequency factors.
+// tab[0 .. n_pairs) / tab[n_pairs .. 2 n_pairs) from the angles rope_angles
+// left in th; ff, if not null, holds the pairs' frequency factors.
 template <class R>
-__device__ inline void rope_table(const R& r, float th0, float th1, uint32_t n_pairs, const float* ff, float* tab,
+__device__ inline void rope_table(const R& r, const float* th, uint32_t n_pairs, const float* ff, float* tab,
                                   uint32_t lane) {
     if (lane < n_pairs) {
-        rope_coeffs(r, th0, lane, ff ? ff[lane] : 1.0f, tab[lane], tab[n_pairs + lane]);
+        rope_coeffs(r, th[lane], lane, ff ? ff[lane] : 1.0f, tab[lane], tab[n_pairs + lane]);
     }
     if (lane + 64 < n_pairs) {
-        rope_coeffs(r, th1, lane + 64, ff ? ff[lane + 64] : 1.0f, tab[lane + 64], tab[n_pairs + lane + 64]);
+        rope_coeffs(r, th[lane + 64], lane + 64, ff ? ff[lane + 64] : 1.0f, tab[lane + 64], tab[n_pairs + lane + 64]);
     }
 }
 

@@ -16,12 +16,14 @@ __global__ __launch_bounds__(256) void rope_kernel(const rope_args a) {
     // -ffp-contract=off build does.
 #pragma clang fp contract(off)
     __shared__ float tab[2 * rope_max_pairs];  // cos, then sin, of each pair
+    __shared__ float th[rope_max_pairs];        // the pairs' angles
     const uint32_t i = blockIdx.x;
     const uint32_t half = a.hd / 2;
     if (threadIdx.x < 64) {
-        float th0, th1;
-        rope_thetas(a.pos + (a.period != 0 ? i % a.period : i), a.theta_scale, half, threadIdx.x, th0, th1);
-        rope_table(a, th0, th1, half, a.freq_factors, tab, threadIdx.x);
+        if (threadIdx.x == 0) {
+            rope_angles(a.pos + (a.period != 0 ? i % a.period : i), a.theta_scale, half, th);
+        }
+        rope_table(a, th, half, a.freq_factors, tab, threadIdx.x);
     }
     __syncthreads();
     // in and out do not overlap (the C ABI checks): every pair's loads are

@@ -46,22 +46,6 @@ namespace syn {
 
 namespace {
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        v = xor_max(v, m);
-    }
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        v = xor_sum(v, m);
-    }
-    return v;
-}
-
 // The sequence a block belongs to: starts[] is non-decreasing, and sequence
 // i owns blocks [starts[i], starts[i+1]). All loads are independent, so they
 // go out as one batch.
@@ -705,14 +689,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const A a) {
             mj[i] = ln + 64 * i < S ? mj[i] : -INFINITY;
             mx = fmaxf(mx, mj[i]);
         }
-        mx = wave_max(mx);
+        mx = wave_reduce_max(mx);
         float sum = 0.0f;
 #pragma unroll
         for (uint32_t i = 0; i < per_lane; ++i) {
             mj[i] = fast_exp2((mj[i] - mx) * c);  // 0 for absent splits
             sum += lj[i] * mj[i];
         }
-        sum = wave_sum(sum);
+        sum = wave_reduce_sum(sum);
         const float inv = 1.0f / sum;
 #pragma unroll
         for (uint32_t i = 0; i < per_lane; ++i) {

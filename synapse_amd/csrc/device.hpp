@@ -152,6 +152,36 @@ __device__ __forceinline__ float sum32(float v) {
     return v + partner32(v);
 }
 
+// Reductions over the whole wave on the VALU, the result the same in every
+// lane: within each quad by DPP (lane ^ 1, lane ^ 2), across the quads of a
+// row by DPP mirrors (lane l with 7 - l, then with 15 - l), then across rows
+// and halves by the permlane swaps above. Every step combines two lanes'
+// values in both of them, and max and addition commute, so all lanes agree
+// bit for bit. (A shuffle per step goes through the LDS crossbar and waits
+// out its latency: six round trips for one reduction.)
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int dpp_quad_xor1 = 0xB1;     // quad_perm [1, 0, 3, 2]
+constexpr int dpp_quad_xor2 = 0x4E;     // quad_perm [2, 3, 0, 1]
+constexpr int dpp_row_half_mirror = 0x141;
+constexpr int dpp_row_mirror = 0x140;
+__device__ __forceinline__ float wave_reduce_max(float v) {
+    v = fmaxf(v, dpp_read<dpp_quad_xor1>(v));
+    v = fmaxf(v, dpp_read<dpp_quad_xor2>(v));
+    v = fmaxf(v, dpp_read<dpp_row_half_mirror>(v));
+    v = fmaxf(v, dpp_read<dpp_row_mirror>(v));
+    return max32(max16(v));
+}
+__device__ __forceinline__ float wave_reduce_sum(float v) {
+    v += dpp_read<dpp_quad_xor1>(v);
+    v += dpp_read<dpp_quad_xor2>(v);
+    v += dpp_read<dpp_row_half_mirror>(v);
+    v += dpp_read<dpp_row_mirror>(v);
+    return sum32(sum16(v));
+}
+
 __device__ __forceinline__ float xor_max(float v, int mask) {
     return fmaxf(v, __shfl_xor(v, mask, wave));
 }

@@ -403,17 +403,42 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
     // E 32-key slices from key t0 (keys past n masked).
     const auto step = [&]<int E>(uint32_t t0) __attribute__((always_inline)) {
         f16v sc[E];
+        // All K operands are read before the first product, and (up to head
+        // dim 64, where the registers are there) the V^T operands right after
+        // the score products: their LDS latency then runs under the products
+        // and the softmax instead of before each product.
+        h8 kop[E][NS];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const char* krow = U.lk + ((t0 + 32 * e + slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                kop[e][st] = *reinterpret_cast<const h8*>(krow + 16 * st);
+            }
+        }
 #pragma unroll
         for (int e = 0; e < E; ++e) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 sc[e][i] = 0.0f;
             }
-            const char* krow = U.lk + ((t0 + 32 * e + slice_key(qi)) * KROWC + H * (KCPR / 2)) * 16;
 #pragma unroll
             for (int st = 0; st < NS; ++st) {
-                sc[e] = mfma32(*reinterpret_cast<const h8*>(krow + 16 * st), qv[st], sc[e]);
+                sc[e] = mfma32(kop[e][st], qv[st], sc[e]);
             }
+        }
+        constexpr bool VPRE = HD <= 64;
+        h8 vop[VPRE ? NT : 1][VPRE ? 2 * E : 1];
+        if constexpr (VPRE) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const char* vrow = U.lv + ((32 * t + qi) * vrowc + t0 / 8 + H) * 16;
+#pragma unroll
+                for (int s2 = 0; s2 < 2 * E; ++s2) {
+                    vop[t][s2] = *reinterpret_cast<const h8*>(vrow + 32 * s2);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         // Register i of slice e holds key t0 + 32e + 16(i/8) + 8H + i%8:
         // masked unless ck = 32e + 16(i/8) + i%8 < n - t0 - 8H.
@@ -436,7 +461,11 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
             const char* vrow = U.lv + ((32 * t + qi) * vrowc + t0 / 8 + H) * 16;
 #pragma unroll
             for (int s2 = 0; s2 < 2 * E; ++s2) {
-                o[t] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[t]);
+                if constexpr (VPRE) {
+                    o[t] = mfma32(vop[t][s2], pv[s2], o[t]);
+                } else {
+                    o[t] = mfma32(*reinterpret_cast<const h8*>(vrow + 32 * s2), pv[s2], o[t]);
+                }
             }
         }
     };

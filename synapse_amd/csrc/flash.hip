@@ -527,47 +527,54 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
         }
     };
 
-    // ---- the tail rows on the vector units ----
-    // Per row: lane l scores keys l, l + 64, ... (f32 sums of binary16
-    // products over the dims in order), the softmax is taken whole (max,
-    // sum, p = e / sum, kept in f32 in LDS), and lane d sums output dim d
-    // over the keys, 8 partial sums by key mod 8 added in order at the end.
+    // ---- the tail rows on the vector units, all four waves ----
+    // Per row: the block scores the keys into s_lds (thread t keys t,
+    // t + 256, ...; f32 sums of binary16 products over the dims in order).
+    // Every wave then takes the softmax whole over all keys (max, sum,
+    // p = e / sum, kept in f32; the waves compute the same values), and wave
+    // v writes back the p of the 64-key blocks u with u % 4 == v. Wave v sums
+    // output dims 64 c + 16 v + l % 16: each 16-lane row of the wave takes a
+    // quarter of the keys (8 partial sums by key mod 8, added in order), and
+    // the four quarters are added across the rows.
     const auto tail_rows = [&](u4 tq) __attribute__((always_inline)) {
         const uint32_t r0 = 32 * n_mq;
         const uint32_t rows = n - r0;
         char* ltail = U.lv + HD * vrowc * 16;
         _Float16* q_lds = reinterpret_cast<_Float16*>(ltail);                        // [tail rows][HD]
-        float* p_lds = reinterpret_cast<float*>(ltail + resident_tail_rows * HD * 2);  // [np]
-        if (static_cast<uint32_t>(ln) < rows * KCPR) {
-            *reinterpret_cast<u4*>(q_lds + (ln / KCPR) * HD + 8 * (ln % KCPR)) = tq;
+        float* s_lds = reinterpret_cast<float*>(ltail + resident_tail_rows * HD * 2);  // [np]
+        const uint32_t wv = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(tid >> 6));
+        if (static_cast<uint32_t>(tid) < rows * KCPR) {  // wave 0's lanes: rows * KCPR <= 32
+            *reinterpret_cast<u4*>(q_lds + (tid / KCPR) * HD + 8 * (tid % KCPR)) = tq;
         }
-        // Written and read by this wave only: its LDS operations complete in order.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        constexpr uint32_t KPL = (NPMAX + 63) / 64;  // keys per lane, at most
+        lds_barrier();
+        constexpr uint32_t KPL = (NPMAX + 63) / 64;            // keys per lane in a wave, at most
+        constexpr uint32_t KPB = (NPMAX + THREADS - 1) / THREADS;  // keys per thread in the block
         typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+        const uint32_t quarter = np / 4;  // a multiple of 8
+        const uint32_t kg = static_cast<uint32_t>(ln) >> 4;
         for (uint32_t i = 0; i < rows; ++i) {
             h8 qr[KCPR];
 #pragma unroll
             for (int ch = 0; ch < KCPR; ++ch) {
                 qr[ch] = *reinterpret_cast<const h8*>(q_lds + i * HD + 8 * ch);
             }
-            // Chunk-major over the lane's keys, so each chunk's reads of all
-            // its keys are in flight together. Rows n..np-1 are zero rows;
-            // lanes past np read the last one.
-            float sj[KPL];
+            // Chunk-major over the thread's keys, so each chunk's reads of
+            // all its keys are in flight together. Rows n..np-1 are zero
+            // rows; threads past np read the last one and store nothing.
+            float sj[KPB];
 #pragma unroll
-            for (uint32_t u = 0; u < KPL; ++u) {
+            for (uint32_t u = 0; u < KPB; ++u) {
                 sj[u] = 0.0f;
             }
 #pragma unroll
             for (int ch = 0; ch < KCPR; ++ch) {
-                h8 kk[KPL];
+                h8 kk[KPB];
 #pragma unroll
-                for (uint32_t u = 0; u < KPL; ++u) {
-                    kk[u] = *reinterpret_cast<const h8*>(U.lk + (min(ln + 64 * u, np - 1) * KROWC + ch) * 16);
+                for (uint32_t u = 0; u < KPB; ++u) {
+                    kk[u] = *reinterpret_cast<const h8*>(U.lk + (min(tid + THREADS * u, np - 1) * KROWC + ch) * 16);
                 }
 #pragma unroll
-                for (uint32_t u = 0; u < KPL; ++u) {
+                for (uint32_t u = 0; u < KPB; ++u) {
 #pragma unroll
                     for (int e = 0; e < 8; e += 2) {
                         sj[u] = __builtin_amdgcn_fdot2(__builtin_bit_cast(fp16x2, h2{qr[ch][e], qr[ch][e + 1]}),
@@ -576,64 +583,75 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
                     }
                 }
             }
+#pragma unroll
+            for (uint32_t u = 0; u < KPB; ++u) {
+                const uint32_t j = tid + THREADS * u;
+                if (j < np) {
+                    s_lds[j] = sj[u];
+                }
+            }
+            lds_barrier();
+            float ej[KPL];
             float mx = -INFINITY;
 #pragma unroll
             for (uint32_t u = 0; u < KPL; ++u) {
-                sj[u] = ln + 64 * u < n ? sj[u] : -INFINITY;
-                mx = fmaxf(mx, sj[u]);
+                const uint32_t j = ln + 64 * u;
+                ej[u] = j < n ? s_lds[j] : -INFINITY;
+                mx = fmaxf(mx, ej[u]);
             }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                mx = xor_max(mx, m);
-            }
+            mx = wave_reduce_max(mx);
             float sum = 0.0f;
 #pragma unroll
             for (uint32_t u = 0; u < KPL; ++u) {
-                sj[u] = fast_exp2((sj[u] - mx) * c);  // 0 past n
-                sum += sj[u];
+                ej[u] = fast_exp2((ej[u] - mx) * c);  // 0 past n
+                sum += ej[u];
             }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                sum = xor_sum(sum, m);
-            }
+            sum = wave_reduce_sum(sum);
             const float inv = 1.0f / sum;
+            lds_barrier();  // every wave has read the scores
 #pragma unroll
             for (uint32_t u = 0; u < KPL; ++u) {
                 const uint32_t j = ln + 64 * u;
-                if (j < np) {
-                    p_lds[j] = sj[u] * inv;
+                if (u % WAVES == wv && j < np) {
+                    s_lds[j] = ej[u] * inv;
                 }
             }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_barrier();
             float* out = a.out + (U.row_base + r0 + i) * a.q_row + U.h * hd;
 #pragma unroll
             for (uint32_t d0 = 0; d0 < HD; d0 += 64) {
-                const uint32_t d = d0 + ln;
+                const uint32_t d = d0 + 16 * wv + (ln & 15);
+                float r = 0.0f;
                 if (d < hd) {
                     // V^T row d: keys 0..np-1 in order (zeros past n).
                     const char* vrow = U.lv + d * vrowc * 16;
                     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-                    for (uint32_t j8 = 0; j8 < np; j8 += 8) {
-                        const h8 vv = *reinterpret_cast<const h8*>(vrow + 2 * j8);
-                        const f4 p0 = *reinterpret_cast<const f4*>(p_lds + j8);
-                        const f4 p1 = *reinterpret_cast<const f4*>(p_lds + j8 + 4);
+                    const uint32_t jb = kg * quarter;
+#pragma unroll 3
+                    for (uint32_t j8 = 0; j8 < quarter; j8 += 8) {
+                        const h8 vv = *reinterpret_cast<const h8*>(vrow + 2 * (jb + j8));
+                        const f4 p0 = *reinterpret_cast<const f4*>(s_lds + jb + j8);
+                        const f4 p1 = *reinterpret_cast<const f4*>(s_lds + jb + j8 + 4);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             acc[e] = fmaf(p0[e], static_cast<float>(vv[e]), acc[e]);
                             acc[4 + e] = fmaf(p1[e], static_cast<float>(vv[4 + e]), acc[4 + e]);
                         }
                     }
-                    float r = acc[0];
+                    r = acc[0];
 #pragma unroll
                     for (int e = 1; e < 8; ++e) {
                         r += acc[e];
                     }
+                }
+                r = sum32(sum16(r));  // quarters (0 + 1) + (2 + 3)
+                if (kg == 0 && d < hd) {
                     out[d] = r;
                 }
             }
-            // The next row rewrites p_lds: every lane's reads above are done.
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (i + 1 < rows) {
+                lds_barrier();  // the next row rewrites s_lds
+            }
         }
     };
 
@@ -642,7 +660,7 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
     store_unit(kc, vc);
     lds_barrier();
     run_unit(qc);
-    if (tail && w0 == 0) {
+    if (tail) {
         tail_rows(tq);
     }
 }

@@ -50,6 +50,23 @@ __device__ __forceinline__ float softmax_probs(const f16v (&sc)[E], float c, flo
 template <int E, int NT>
 __device__ __forceinline__ void online_softmax(const f16v (&sc)[E], float c, float& m_run, float& l_run,
                                                f16v (&o)[NT], h8 (&pv)[2 * E]) {
+    // No query of the wave has a max yet (a sweep's first step): take the
+    // max first. The optimistic pass would go to the rescale path for every
+    // query and compute the probabilities twice; this gives the same values
+    // (the sum and O are still 0, so the rescale would not change them).
+    if (__builtin_amdgcn_ballot_w64(m_run != -INFINITY) == 0) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                tmax = fmaxf(tmax, sc[e][i]);
+            }
+        }
+        m_run = max32(tmax);
+        l_run += softmax_probs<E>(sc, c, m_run, pv);
+        return;
+    }
     float psum = softmax_probs<E>(sc, c, m_run, pv);
     const bool grow = m_run == -INFINITY || !(psum <= 256.0f);
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {

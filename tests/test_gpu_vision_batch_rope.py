@@ -112,14 +112,19 @@ def _tail_rows(arena, n, hd, batch, n_heads, images):
             assert tail < 1e-5, (b, n, hd, tail)
 
 
-@pytest.mark.parametrize("n,hd", [(257, 64), (258, 64), (1, 64), (2, 64), (513, 32), (514, 32), (129, 96)])
+@pytest.mark.parametrize("n,hd", [(257, 64), (258, 64), (1, 64), (2, 64), (513, 32), (514, 32), (1, 32),
+                                  (129, 96), (2, 96), (1, 128), (2, 128)])
 def test_vision_tail_rows_keep_f32_probabilities(arena, n, hd):
     """The vector-unit rows (the last tile's one or two rows) keep p in f32
     and sum in f32 over binary16-exact inputs, as the oracle does: within
     1e-5 of the largest output, where the matrix-core rows (p rounded to
-    binary16) are held to the parity bound only. A wrong key, a dropped
-    key or a wrong head would miss by orders of magnitude. Few units: one
-    per 4-wave block, tail rows when the query tiles are 1 mod 4."""
+    binary16) are held to the parity bound only. The block's four waves
+    share them (keys scored across the block, output dims in 16-dim slices
+    per wave, key quarters per 16-lane row), so a wrong key, a dropped key
+    quarter, a wrong dim slice or a wrong head would miss by orders of
+    magnitude; head dims 32 to 128 cover one and two 64-dim passes, with
+    idle slices at 32 and 96. Few units: one per 4-wave block, tail rows
+    when the query tiles are 1 mod 4."""
     _tail_rows(arena, n, hd, 2, 3, range(2))
 
 

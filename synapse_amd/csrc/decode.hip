@@ -32,8 +32,9 @@
 // never see them), and the handoff -- store acknowledged, arrival counter,
 // poll, partial loads -- costs three or four loaded memory round trips,
 // more than the second launch. The merge stages through LDS: one wave turns
-// the splits' (max, sum) into weights with shuffles, then all threads stream
-// the partial outputs with independent 16-byte loads. Each output sums its
+// the splits' (max, sum) into weights (its wave-wide max and sum by DPP and
+// permlane swaps), then all threads stream the partial outputs with
+// independent 16-byte loads. Each output sums its
 // splits in a fixed order, so results are deterministic.
 //
 // A single-token step passes its new K, V row (k_new, v_new): the block whose

@@ -337,7 +337,7 @@ __global__ __launch_bounds__(512) void gemv_q_kernel(const uint8_t* w, const flo
             const uint32_t o = o0 + t / nb * o_step;
 #pragma unroll
             for (int j = 0; j < NR; ++j) {
-                const float s = wave_sum_q(acc[j]);
+                const float s = wave_reduce_sum(acc[j]);
                 if (ln == 0 && r0 + j < n) {
                     out[static_cast<std::size_t>(r0 + j) * rows + o] = bias != nullptr ? s + bias[o] : s;
                 }

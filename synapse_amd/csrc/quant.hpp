@@ -20,13 +20,6 @@ __device__ __forceinline__ float half_at(const uint8_t* p) {
     return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 }
 
-__device__ __forceinline__ float wave_sum_q(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        v += __shfl_xor(v, m, wave);
-    }
-    return v;
-}
 
 // (scale, min) of sub-block j of a Q4_K super-block's 12 packed bytes.
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& sc, int& m) {

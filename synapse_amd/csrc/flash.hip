@@ -249,8 +249,9 @@ __host__ __device__ constexpr uint32_t resident_lds_bytes(uint32_t n, uint32_t h
 }
 // A last query tile of at most this many rows that would be a third tile on
 // one wave (query tiles = 1 mod 4, as 257 rows make 9) is computed on the
-// vector units instead, by that wave, after its tiles, so every wave sweeps
-// the same number of tiles. Its LDS: the rows' q and one probability row.
+// vector units instead, by all four waves after their tiles, so every wave
+// sweeps the same number of tiles. Its LDS: the rows' q and one row of
+// scores (then probabilities).
 constexpr uint32_t resident_tail_rows = 2;
 __host__ __device__ constexpr uint32_t resident_tail_bytes(uint32_t n, uint32_t hdp) {
     return resident_tail_rows * hdp * 2 + (n + 31) / 32 * 32 * 4;
@@ -364,8 +365,8 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
                                                        : buffer_oob);
             }
         }
-        // The tail rows' q, chunk ln (row ln / KCPR), for the wave that
-        // computes them.
+        // The tail rows' q, chunk ln (row ln / KCPR); wave 0's copy goes to
+        // LDS for the block.
         const uint32_t tr = 32 * n_mq + ln / KCPR, tc = ln % KCPR;
         tq = buffer_load16(U.q_res, tail && tr < n && 8 * tc < hd ? (tr * a.q_row + U.h * hd + 8 * tc) * 2
                                                                   : buffer_oob);

@@ -285,7 +285,12 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
     constexpr uint32_t NPMAX = resident_max_keys(HD);
     constexpr uint32_t KC = (NPMAX * KCPR + THREADS - 1) / THREADS;      // K chunks per thread and unit
     constexpr uint32_t VC = (NPMAX / 2 * KCPR + THREADS - 1) / THREADS;  // V key pairs per thread and unit
-    constexpr uint32_t QT = (NPMAX / 32 + WAVES - 1) / WAVES;  // q tiles per wave, at most
+    // Up to head dim 64 a wave stages only its first query tile's q and
+    // loads each later tile's during the tile before (the staging, which
+    // every wave waits for, is then ~16 % smaller); above, the registers are
+    // not there, and the first QT tiles are staged.
+    constexpr bool QPRE = HD <= 64;
+    constexpr uint32_t QT = QPRE ? 1 : (NPMAX / 32 + WAVES - 1) / WAVES;  // q tiles staged per wave
     extern __shared__ __attribute__((aligned(16))) char lds[];
 
     const int tid = threadIdx.x;
@@ -471,10 +476,12 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
         }
     };
     const auto run_unit = [&](const u4 (&qc)[QT][NS]) __attribute__((always_inline)) {
+        u4 qn[QPRE ? NS : 1];  // the next tile's q, loaded while this tile computes
         for (uint32_t t = 0; w0 + WAVES * t < n_mq; ++t) {
             const uint32_t tq = w0 + WAVES * t;
             const uint32_t my_q = 32 * tq + qi;
-            // The first QT tiles' q came with the staging; later ones load here.
+            // The first QT tiles' q came with the staging; later ones were
+            // loaded during the tile before (QPRE) or load here.
             if (t < QT) {
 #pragma unroll
                 for (uint32_t tt = 0; tt < QT; ++tt) {
@@ -485,12 +492,27 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
                         }
                     }
                 }
+            } else if constexpr (QPRE) {
+#pragma unroll
+                for (int st = 0; st < NS; ++st) {
+                    qv[st] = as_h8(qn[st]);
+                }
             } else {
 #pragma unroll
                 for (int st = 0; st < NS; ++st) {
                     const uint32_t d0 = H * (HD / 2) + 8 * st;
                     qv[st] = as_h8(buffer_load16(U.q_res, my_q < n && d0 < hd ? (my_q * a.q_row + U.h * hd + d0) * 2
                                                                               : buffer_oob));
+                }
+            }
+            if constexpr (QPRE) {
+                const uint32_t my_q1 = my_q + 32 * WAVES;
+#pragma unroll
+                for (int st = 0; st < NS; ++st) {
+                    const uint32_t d0 = H * (HD / 2) + 8 * st;
+                    qn[st] = buffer_load16(U.q_res, tq + WAVES < n_mq && my_q1 < n && d0 < hd
+                                                        ? (my_q1 * a.q_row + U.h * hd + d0) * 2
+                                                        : buffer_oob);
                 }
             }
 #pragma unroll

@@ -10,10 +10,11 @@ distinct KV states (>= 512 MiB together, as a real model's 32 layers are),
 so K and V come from HBM, not the 256 MB Infinity Cache. Inputs are resident
 in HBM before the timed region.
 
-One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time,
-steps called one by one through the C ABI; "extra" also has the same steps
-replayed from a HIP graph, which measures the same), roofline of the decode
-op (the same HIP-event time on the arena's stream),
+One JSON line on stdout: value = decode GB/s (algorithmic bytes / step time;
+the K timed steps are captured into one HIP graph and the timed region is
+its launch, so the kernels pace it, not Python's per-call dispatch; "extra"
+has the same steps called one by one and their wall time), roofline of the
+decode op (the same HIP-event time on the arena's stream),
 the CPU oracle timed on this host, and the other configs' figures (prefill
 TFLOP/s, ragged decode, ViT, quantized GEMV and GEMM) under "extra". --copy-bytes N adds one arena
 copy of N bytes, the calibration dispatch for rocprofv3 --pmc FETCH_SIZE /
@@ -81,7 +82,18 @@ def log(msg: str) -> None:
 
 
 def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int, graph: bool = True):
-    """Config 2: returns (ms_per_step, graph-replayed ms_per_step or None, details)."""
+    """Config 2: returns (ms_per_step, details).
+
+    The timed region is exactly `steps` steps; step i runs on KV state
+    (warmup + i) % layers, so the rotation continues past the warm-up's
+    states and the timed steps read caches that are not the most recently
+    touched. With graph (the default) the steps are captured beforehand into
+    one HIP graph of 2 * steps kernel nodes, uploaded, and the timed region is
+    that graph's one launch: the GPU runs the steps back to back, paced by
+    the kernels, not by this process's per-call dispatch. Without it
+    (profiler runs: rocprofv3's kernel trace once ended a process that
+    captured graphs with a segmentation fault) the steps are called one by
+    one through the C ABI. `details` has the per-call figures either way."""
     row = cfg.n_kv * cfg.head_dim
     max_ctx = cfg.ctx + 1
     state = capi.kv_state_bytes(max_ctx, cfg.n_kv, cfg.head_dim)
@@ -102,55 +114,59 @@ def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int,
     arena.sync()
     stream = arena.stream
     L = lib()
-    for i in range(warmup):
-        check(L.syn_hip_attention(arena.handle, ctypes.byref(descs[i % layers])))
-    arena.sync()
-    # Timed region: whole steps back to back, each called through the C ABI
-    # (two launches: the split kernel, which appends the row itself, and the
-    # merge kernel).
+    byref = [ctypes.byref(d) for d in descs]
+    step = lambda i: check(L.syn_hip_attention(arena.handle, byref[i % layers]))  # noqa: E731
     t0, t1 = hip.events(2)
+
+    # Per-call figures first (untimed as far as the headline goes): the same
+    # steps called one by one from this Python loop, which the host's
+    # dispatch can pace, and the spread of single bracketed calls.
+    n_eager = max(steps, 2 * layers)
+    for i in range(layers):
+        step(i)
+    arena.sync()
     hip.record(t0, stream)
     w0 = time.perf_counter()
-    for i in range(steps):
-        check(L.syn_hip_attention(arena.handle, ctypes.byref(descs[i % layers])))
+    for i in range(n_eager):
+        step(i)
     hip.record(t1, stream)
-    step_ms = hip.ms(t0, t1) / steps
-    wall_ms = (time.perf_counter() - w0) * 1e3 / steps
-    # Per-launch event pairs, for the spread of single launches.
-    evs = hip.events(2 * steps)
-    for i in range(steps):
-        d = descs[i % layers]
+    eager_ms = hip.ms(t0, t1) / n_eager
+    wall_ms = (time.perf_counter() - w0) * 1e3 / n_eager
+    evs = hip.events(2 * n_eager)
+    for i in range(n_eager):
         hip.record(evs[2 * i], stream)
-        check(L.syn_hip_attention(arena.handle, ctypes.byref(d)))
+        step(i)
         hip.record(evs[2 * i + 1], stream)
-    kern = [hip.ms(evs[2 * i], evs[2 * i + 1]) for i in range(steps)]
+    kern = [hip.ms(evs[2 * i], evs[2 * i + 1]) for i in range(n_eager)]
     out = arena.download(descs[0].out_offset, (qsz,), np.float32)
     assert np.all(np.isfinite(out))
-    # The same steps replayed from a HIP graph: one graph holds one step per
-    # KV state (as a model's decode step holds one per layer), replayed until
-    # `steps` steps have run; one host call per graph instead of per step. It
-    # shows whether host launch overhead shapes the per-call figure.
-    # Profiling runs skip it (--no-graph): rocprofv3's kernel trace ended
-    # this process with a segmentation fault when the bench captured graphs.
-    graph_ms, reps = None, 0
+
+    det = {"eager_ms_per_step": eager_ms, "wall_ms_per_step": wall_ms, "kernel_ms_median": float(np.median(kern)),
+           "timing": "HIP-graph launch of the timed steps" if graph else "steps called one by one"}
     if graph:
-        byref = [ctypes.byref(d) for d in descs]
-        reps = max(1, steps // layers)
-        with capi.HipGraph(arena, lambda: [check(L.syn_hip_attention(arena.handle, r)) for r in byref]) as hg:
-            for _ in range(2):
-                hg.launch()
+        with capi.HipGraph(arena, lambda: [step(warmup + i) for i in range(steps)]) as hg:
+            hg.upload()
+            for i in range(warmup):
+                step(i)
             arena.sync()
             hip.record(t0, stream)
-            for _ in range(reps):
-                hg.launch()
+            hg.launch()
             hip.record(t1, stream)
-            graph_ms = hip.ms(t0, t1) / (reps * layers)
+            step_ms = hip.ms(t0, t1) / steps
             arena.sync()
-        out_g = arena.download(descs[0].out_offset, (qsz,), np.float32)
+        out_g = arena.download(descs[warmup % layers].out_offset, (qsz,), np.float32)
         assert np.array_equal(out_g.view(np.uint32), out.view(np.uint32))
+    else:
+        for i in range(warmup):
+            step(i)
+        arena.sync()
+        hip.record(t0, stream)
+        for i in range(steps):
+            step(warmup + i)
+        hip.record(t1, stream)
+        step_ms = hip.ms(t0, t1) / steps
     arena.close()
-    return step_ms, graph_ms, {"wall_ms_per_step": wall_ms, "kernel_ms_median": float(np.median(kern)),
-                               "kernel_ms_mean_bracketed": float(np.mean(kern)), "graph_steps": reps * layers}
+    return step_ms, det
 
 
 def bench_decode_rope(hip: Hip, cfg: wl.Decode, steps: int, layers: int):
@@ -284,24 +300,34 @@ def bench_ragged(hip: Hip, cfg: wl.Ragged, reps: int):
 
 
 def bench_vision(hip: Hip, cfg: wl.Vision, reps: int):
+    """Config 5 over `sets` distinct copies of its inputs and outputs
+    (>= 256 MB together, past the 256 MB Infinity Cache), launch i on copy
+    i % sets, so each launch reads its Q, K, V from HBM and writes its
+    output there. Returns (ms per launch, copies rotated)."""
     rows = cfg.batch * cfg.n
     size = cfg.n_heads * cfg.head_dim
-    arena = Arena(rows * size * (3 * 2 + 4) + (8 << 20))
+    per_set = capi.align(rows * size * 2) * 3 + capi.align(rows * size * 4)
+    sets = max(4, -(-(256 << 20) // per_set))
+    arena = Arena(sets * per_set + (8 << 20))
     q, k, v = wl.vision_inputs(cfg)
-    d = SelfDesc(q_offset=arena.put(q.astype(np.float16)), k_offset=arena.put(k.astype(np.float16)),
-                 v_offset=arena.put(v.astype(np.float16)), out_offset=arena.alloc(rows * size * 4), n=cfg.n,
-                 batch=cfg.batch, n_heads=cfg.n_heads, head_dim=cfg.head_dim, scale=cfg.scale, in_dtype=SYN_F16)
+    descs = []
+    for _ in range(sets):
+        descs.append(SelfDesc(q_offset=arena.put(q.astype(np.float16)), k_offset=arena.put(k.astype(np.float16)),
+                              v_offset=arena.put(v.astype(np.float16)), out_offset=arena.alloc(rows * size * 4),
+                              n=cfg.n, batch=cfg.batch, n_heads=cfg.n_heads, head_dim=cfg.head_dim,
+                              scale=cfg.scale, in_dtype=SYN_F16))
     L = lib()
-    check(L.syn_hip_self_attention(arena.handle, ctypes.byref(d)))
+    for d in descs:
+        check(L.syn_hip_self_attention(arena.handle, ctypes.byref(d)))
     arena.sync()
     t0, t1 = hip.events(2)
     hip.record(t0, arena.stream)
-    for _ in range(reps):
-        check(L.syn_hip_self_attention(arena.handle, ctypes.byref(d)))
+    for i in range(reps):
+        check(L.syn_hip_self_attention(arena.handle, ctypes.byref(descs[i % sets])))
     hip.record(t1, arena.stream)
     ms = hip.ms(t0, t1) / reps
     arena.close()
-    return ms
+    return ms, sets
 
 
 # Quantized GEMV shapes of a Llama-3-8B Q4_K_M decode step (one token):
@@ -541,10 +567,13 @@ def main() -> int:
     if only in (None, "vision"):
         vcfg = wl.C5
         log(f"vision {vcfg.name}")
-        vms = bench_vision(hip, vcfg, 50)
-        extra["vision"] = {"us": round(vms * 1e3, 2), "tflops": round(vcfg.flops() / (vms * 1e-3) / 1e12, 1),
-                           "gbs": round(vcfg.bytes() / (vms * 1e-3) / 1e9, 1),
-                           "images_per_s": round(vcfg.batch / (vms * 1e-3), 0)}
+        vms, vsets = bench_vision(hip, vcfg, 48)
+        vgbs = vcfg.bytes() / (vms * 1e-3) / 1e9
+        vtf = vcfg.flops() / (vms * 1e-3) / 1e12
+        extra["vision"] = {"us": round(vms * 1e3, 2), "tflops": round(vtf, 1),
+                           "frac_of_f16_peak": round(vtf / MFMA_F16_PEAK_TFS, 4), "gbs": round(vgbs, 1),
+                           "frac_of_hbm": round(vgbs / HBM_PEAK_GBS, 4), "bytes": vcfg.bytes(),
+                           "input_sets_rotated": vsets, "images_per_s": round(vcfg.batch / (vms * 1e-3), 0)}
         log(f"vision: {vms * 1e3:.1f} us, {extra['vision']['tflops']:.0f} TFLOP/s")
     if only in (None, "gemv"):
         extra["gemv_q"] = bench_gemv(hip, 400)
@@ -555,20 +584,19 @@ def main() -> int:
 
     cfg = wl.C2
     log(f"decode {cfg.name}: {args.steps} steps, {args.warmup} warmup, {args.layers} rotating KV states")
-    step_ms, graph_ms, det = bench_decode(hip, cfg, args.steps, args.warmup, args.layers, graph=not args.no_graph)
-    kern_ms = step_ms
+    step_ms, det = bench_decode(hip, cfg, args.steps, args.warmup, args.layers, graph=not args.no_graph)
     nbytes = cfg.kv_bytes()
     value = nbytes / (step_ms * 1e-3) / 1e9
-    achieved = nbytes / (kern_ms * 1e-3) / 1e9
-    replay = f" ({graph_ms * 1e3:.2f} us/step replayed from a HIP graph)" if graph_ms is not None else ""
-    log(f"decode: {step_ms * 1e3:.2f} us/step -> {value:.0f} GB/s{replay}")
+    log(f"decode: {step_ms * 1e3:.2f} us/step -> {value:.0f} GB/s ({det['timing']}); called one by one: "
+        f"{det['eager_ms_per_step'] * 1e3:.2f} us/step, wall {det['wall_ms_per_step'] * 1e3:.2f} us/step")
     extra["decode_rope"] = bench_decode_rope(hip, cfg, 400, args.layers)
     log(f"decode with RoPE: {extra['decode_rope']}")
     extra.update({"decode_step_us": round(step_ms * 1e3, 3),
-                  "decode_graph_step_us": round(graph_ms * 1e3, 3) if graph_ms is not None else None,
-                  "decode_tokens_per_s_32_layers": round(1e3 / (step_ms * 32), 1),
+                  "decode_timing": det["timing"],
+                  "decode_eager_step_us": round(det["eager_ms_per_step"] * 1e3, 3),
                   "decode_wall_us_per_step": round(det["wall_ms_per_step"] * 1e3, 3),
                   "decode_single_step_us_median": round(det["kernel_ms_median"] * 1e3, 3),
+                  "decode_tokens_per_s_32_layers": round(1e3 / (step_ms * 32), 1),
                   "decode_kernels_per_step": 2})
 
     line = {
@@ -579,9 +607,10 @@ def main() -> int:
         "config": {"workload": "config 2: Llama-3-8B decode attention, H=32, Hkv=8, hd=128, 4096 cached rows "
                                "+ 1 appended (append + attend per step)",
                    "kv_states_rotated": args.layers, "bytes_per_step": nbytes},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
-                     "kernel": "decode op (split-KV kernel + merge kernel), HIP events over the timed region"},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
+                     "kernel": "decode op (split-KV kernel + merge kernel, 2 launches per step), HIP events "
+                               "around the timed steps (" + det["timing"] + ")"},
         "cpu_baseline": None,
         "extra": extra,
     }

@@ -653,7 +653,8 @@ int syn_hip_attention_rope(syn_arena* a, const syn_attn_desc* d, const syn_attn_
         rp.attn_factor = r->attn_factor;
         rp.corr_low = r->corr_low;
         rp.corr_high = r->corr_high;
-        rp.q_scale = r->temp_floor_len != 0 ? syn::attn_temperature(d->pos, r->temp_scale, r->temp_floor_len) : 1.0f;
+        rp.temp_scale = r->temp_scale;
+        rp.temp_floor_len = r->temp_floor_len;
         return attend_checked(a, d, true, nullptr, &rp);
     }
     // The separate ops, into the caller's rows.

@@ -265,12 +265,15 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         }
         lds_barrier();
         const bool normal = a_rope(a).mode == 0;
+        const float q_scale = a_rope(a).temp_floor_len != 0
+                                  ? attn_temperature(new_t, a_rope(a).temp_scale, a_rope(a).temp_floor_len)
+                                  : 1.0f;
         const uint32_t rows = group + (new_here ? 1u : 0u);  // q heads, then the new K row
         for (uint32_t u = tid; u < rows * half; u += 256) {
             const uint32_t row = u / half;
             const uint32_t pr = u % half;
             float* x = row < group ? reinterpret_cast<float*>(lds_bytes) + row * hd : reinterpret_cast<float*>(new_lds);
-            const float f = row < group ? a_rope(a).q_scale : 1.0f;
+            const float f = row < group ? q_scale : 1.0f;
             const uint32_t i0 = normal ? 2 * pr : pr;
             const uint32_t i1 = normal ? i0 + 1 : pr + half;
             const float cs = rope_tab[pr], sn = rope_tab[half + pr];

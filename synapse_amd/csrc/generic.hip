@@ -83,16 +83,22 @@ __global__ __launch_bounds__(64) void generic_kernel(const flash_args a) {
     }
 }
 
-// Image-encoder attention on f32 rows with the reference's arithmetic
-// (self_attend_head, S/kernels/attention.hpp:324-486): a score is
-// acc = fma(q_d, k_d, acc) over d from 0, times scale; softmax over the
-// image's keys in f32 with the max subtracted, a double sum and a multiply by
-// float(1 / sum) (S/kernels/elementwise.hpp:174-201); an output element is
-// acc = fma(p_j, v_j, acc) over j from 0. No binary16 anywhere, so f32 inputs
-// keep f32 precision end to end. One wave per (query row, head, image): lane
-// l scores keys l, l + 64, ... (each chain in order), the probabilities sit
-// in LDS, and lane l then sums output dims l, l + 64, ... over the keys in
-// order. The f16-input and long-image shapes take the matrix-core kernel.
+// Image-encoder attention on f32 rows, close to the reference's arithmetic
+// (self_attend_head, S/kernels/attention.hpp:324-486). What follows the
+// reference's order: a score is acc = fma(q_d, k_d, acc) over d from 0,
+// times scale; the max is subtracted (exact in any order); each probability
+// is e_j * float(1 / sum); an output element is acc = fma(p_j, v_j, acc) over
+// j from 0. What does not: the exponential is the device's expf, not the
+// host libm's std::exp, and the double sum of the exponentials is taken per
+// lane over keys l, l + 64, ... and then across the lanes by an xor tree,
+// where the reference adds them in key order (S/kernels/elementwise.hpp:
+// 190-194). Both differ from the reference in the last bits only, and no
+// binary16 rounding happens anywhere, so f32 inputs keep f32 precision end to
+// end (the tests hold it within 2e-6 of the largest output). One wave per
+// (query row, head, image): lane l scores keys l, l + 64, ... (each chain in
+// order), the probabilities sit in LDS, and lane l then sums output dims
+// l, l + 64, ... over the keys in order. The f16-input and long-image shapes
+// take the matrix-core kernel.
 __global__ __launch_bounds__(64) void self_f32_kernel(const flash_args a) {
     extern __shared__ float probs[];  // n
     const int ln = threadIdx.x;

@@ -80,16 +80,18 @@ struct decode_batch_args {
 
 // RoPE and the attention temperature inside a single-sequence decode step:
 // the step's q row and new K row are rotated as op_rope rotates them
-// (S/kernels/attention.hpp:89-129), then q is multiplied by q_scale
-// (op_attn_temperature's factor at the step's position, S/kernels/
-// elementwise.hpp:66-72; 1 for none), before q's rounding to binary16. The
-// same arithmetic as the rope kernel, so the fused step equals the unfused
-// one bit for bit. q and the new rows are f32.
+// (S/kernels/attention.hpp:89-129), then q is multiplied by the
+// op_attn_temperature factor of the step's position (S/kernels/
+// elementwise.hpp:66-72; none when temp_floor_len is 0), computed on the
+// device by attn_temperature, before q's rounding to binary16. The same
+// arithmetic as the rope and temperature kernels, so the fused step equals
+// the unfused one bit for bit. q and the new rows are f32.
 struct rope_params {
     const float* freq_factors;  // head_dim / 2 floats, or nullptr
     uint32_t mode;              // 0 normal (pairs 2i, 2i + 1), 1 neox (pairs i, i + hd/2)
     float theta_scale, freq_scale, ext_factor, attn_factor, corr_low, corr_high;
-    float q_scale;
+    float temp_scale;           // attention temperature: 1 + temp_scale ln(floor(pos / temp_floor_len) + 1)
+    uint32_t temp_floor_len;    //   0: no temperature
 };
 
 struct decode_rope_args {
@@ -172,9 +174,12 @@ __device__ __forceinline__ float rope_second(float x0, float x1, float cs, float
 
 // The attention temperature of position pos (kernels::attn_temperature,
 // S/kernels/elementwise.hpp:66-72): a float quotient floored, the logarithm
-// in double, the result rounded to float. The same expression on the host
-// (the fused decode step's factor) and on the device (the row kernel).
-__host__ __device__ inline float attn_temperature(uint32_t pos, float scale, uint32_t floor_len) {
+// in double, the result rounded to float; the double multiply and add round
+// on their own, as the reference's -ffp-contract=off build computes them.
+// Only device code calls it (the row kernel and the fused decode step), so
+// both use the same logarithm and agree bit for bit.
+__device__ inline float attn_temperature(uint32_t pos, float scale, uint32_t floor_len) {
+#pragma clang fp contract(off)
     const float q = floorf(static_cast<float>(pos) / static_cast<float>(floor_len));
     return static_cast<float>(log(static_cast<double>(q) + 1.0) * static_cast<double>(scale) + 1.0);
 }

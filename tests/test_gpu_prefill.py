@@ -91,6 +91,33 @@ def test_prefill_llama3_8b_2048(arena):
     assert_close(got, want, what="C3 all rows")
 
 
+@pytest.mark.parametrize("n,pos", [(2048, 0), (300, 0), (1000, 77)])
+def test_prefill_is_deterministic(arena, n, pos):
+    """Two runs of the same attend over the same cache give the same bits:
+    config 3's shape (every 8-wave block merges its later tile's two
+    partials through LDS in a fixed order), an odd tile count (the middle
+    tile, whose block has one tile) and a run after cached rows. The
+    reference pins thread-count invariance bit for bit
+    (tests/sdk/llama_threads.cpp:32-58)."""
+    n_heads, n_kv, hd = 32, 8, 128
+    cfg = wl.Prefill("case", n_heads, n_kv, hd, pos + n, 500000.0)
+    q, k, v = wl.prefill_inputs(cfg, seed=n + pos, f16_exact=True)
+    mark = arena.top
+    cache = capi.kv_state(arena, pos + n, n_kv, hd)
+    scratch = scratch_for(arena, n_heads, n_kv, hd, pos + n)
+    if pos:
+        attention(arena, cache, scratch, q[:pos], k[:pos], v[:pos], 0, n_heads, cfg.scale, SYN_F16, SYN_F16)
+    a = attention(arena, cache, scratch, q[pos:], k[pos:], v[pos:], pos, n_heads, cfg.scale, SYN_F16, SYN_F16)
+    b = attention(arena, cache, scratch, q[pos:], None, None, pos, n_heads, cfg.scale, SYN_F16, SYN_F16,
+                  append=False)
+    c = attention(arena, cache, scratch, q[pos:], None, None, pos, n_heads, cfg.scale, SYN_F16, SYN_F16,
+                  append=False)
+    arena.top = mark
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(b.view(np.uint32), c.view(np.uint32))
+
+
 def test_prefill_21_tiles_after_cached_rows(arena):
     """A run of 2600 tokens (21 query tiles of 128, the last ragged) after
     300 cached rows: every row against the oracle."""

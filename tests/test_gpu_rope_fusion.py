@@ -110,6 +110,18 @@ def test_decode_step_fused_equals_separate_calls(arena, n_heads, n_kv, hd, ctx, 
     assert not rotated[0].any() and not rotated[1].any()
 
 
+@pytest.mark.parametrize("temp", [(0.37, 3), (0.1, 8192), (1.7, 1)])
+def test_fused_temperature_equals_separate_over_positions(arena, temp):
+    """The fused step's temperature factor is computed on the device by the
+    same function as syn_hip_attn_temperature's rows: bit-equal outputs and
+    cache rows at many positions, with a floor length above 1 and a nonzero
+    scale (factors change every floor_len positions)."""
+    for ctx in (1, 2, 3, 5, 8, 13, 21, 34, 55, 89, 127, 128, 129, 200, 377, 610, 987, 1597, 2584, 4095, 4096):
+        got, want, cache_f, cache_s, _, _ = _layer(arena, 8, 2, 64, ctx, 1, 0, False, False, temp, seed=ctx)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), ctx
+        assert np.array_equal(cache_f[0], cache_s[0]) and np.array_equal(cache_f[1], cache_s[1]), ctx
+
+
 @pytest.mark.parametrize("n_heads,n_kv,hd,ctx,n", [(32, 8, 128, 100, 37), (4, 2, 12, 20, 1), (6, 2, 20, 0, 5)])
 def test_unfused_runs_make_the_separate_calls(arena, n_heads, n_kv, hd, ctx, n):
     """Several tokens (prefill) and head sizes the split-KV kernel does not

@@ -24,9 +24,10 @@ def arena():
 
 # ---- bidirectional ----------------------------------------------------------
 
-# f32 rows take a kernel with the reference's own f32 arithmetic: the same
-# fma chains in the same order as the oracle, so only the exponential's last
-# bits differ.
+# f32 rows take a kernel with the reference's f32 arithmetic: the score and
+# output fma chains in the oracle's order; the exponential (device expf) and
+# the order of the double sum of the exponentials (per lane, then across
+# lanes) differ, which moves only the last bits.
 F32_BOUND = 2e-6
 
 
@@ -52,6 +53,23 @@ def test_vision_clip_vit_l14(arena):
     inputs ~ N(0, 0.5^2); every image checked against the oracle."""
     c = wl.C5
     _vision(arena, c.n, c.batch, c.n_heads, c.head_dim, SYN_F16, c.sigma, seed=wl.SEED)
+
+
+@pytest.mark.parametrize("n,batch,n_heads,hd", [(257, 32, 16, 64), (257, 3, 5, 128), (1000, 2, 3, 64)])
+def test_vision_is_deterministic(arena, n, batch, n_heads, hd):
+    """Two launches on the same f16 inputs give the same bits. Config 5's
+    shape (257 rows: the head-resident kernel with its tail rows summed in
+    quarters across the waves), a head-resident shape at hd 128 and a tiled
+    one. The reference pins split invariance bit for bit
+    (tests/sdk/kernels_vision.cpp:252-263; tests/sdk/clip_golden.cpp:37-44)."""
+    g = wl.rng(n + hd)
+    shape = (batch * n, n_heads * hd)
+    q, k, v = (wl.normal(g, shape, 0.5).astype(np.float16).astype(np.float32) for _ in range(3))
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    a = self_attention(arena, q, k, v, n, batch, n_heads, scale, SYN_F16)
+    b = self_attention(arena, q, k, v, n, batch, n_heads, scale, SYN_F16)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 @pytest.mark.parametrize("n,hd", [(37, 8), (1, 8), (6, 16), (50, 24), (130, 64), (257, 128), (64, 256),
@@ -143,7 +161,7 @@ def test_vision_generic_head_dims(arena, n, hd):
 
 # ---- ragged batched decode ---------------------------------------------------
 
-def _ragged(arena, lengths, n_heads, n_kv, hd, seed):
+def _ragged(arena, lengths, n_heads, n_kv, hd, seed, repeats=1):
     scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
     g = wl.rng(seed)
     row = n_kv * hd
@@ -163,12 +181,20 @@ def _ragged(arena, lengths, n_heads, n_kv, hd, seed):
     arr = seq_array(seqs)
     need = int(lib().syn_hip_attend_batch_scratch_bytes(arr, len(seqs), n_heads))
     scratch = arena.alloc(max(need, 256))
-    check(lib().syn_hip_attend_batch(arena.handle, arr, len(seqs), n_heads, scale, SYN_F32, scratch, need))
-    for i, s in enumerate(seqs):
-        got = arena.download(s.out_offset, (1, n_heads * hd), np.float32)
+    runs = []
+    for _ in range(repeats):
+        check(lib().syn_hip_attend_batch(arena.handle, arr, len(seqs), n_heads, scale, SYN_F32, scratch, need))
+        runs.append([arena.download(s.out_offset, (1, n_heads * hd), np.float32) for s in seqs])
+    for i, got in enumerate(runs[0]):
         assert_close(got, refs[i], what=f"sequence {i} (length {lengths[i]})")
         if lengths[i] <= SHORT_ROWS:
             assert_p_rounded_normalised(got, refs[i], n_heads, what=f"sequence {i} (length {lengths[i]})")
+    # Every run of the same launch gives the same bits: fixed splits and a
+    # fixed merge order (the reference pins thread-count invariance bit for
+    # bit, tests/sdk/llama_threads.cpp:32-58).
+    for r in runs[1:]:
+        for i, got in enumerate(r):
+            assert np.array_equal(got.view(np.uint32), runs[0][i].view(np.uint32)), f"sequence {i} differs"
     arena.top = mark
 
 
@@ -178,9 +204,10 @@ SHORT_ROWS = 128
 
 
 def test_ragged_decode_config4(arena):
-    """Config 4 at full size: 16 sequences, lengths U[512, 32768] from the seed."""
+    """Config 4 at full size: 16 sequences, lengths U[512, 32768] from the
+    seed; the launch runs twice and must give the same bits both times."""
     c = wl.C4
-    _ragged(arena, [int(x) for x in c.lengths()], c.n_heads, c.n_kv, c.head_dim, seed=wl.SEED)
+    _ragged(arena, [int(x) for x in c.lengths()], c.n_heads, c.n_kv, c.head_dim, seed=wl.SEED, repeats=2)
 
 
 def test_ragged_decode_many_short(arena):

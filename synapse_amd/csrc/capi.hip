@@ -192,7 +192,10 @@ int run_decode(syn_arena* a, const syn::decode_seq* seqs, uint32_t n, uint32_t n
     for (uint32_t i = 0; i < n; ++i) {
         table[i] = seqs[i];
         table[i].block0 = splits;
-        table[i].n_splits = (seqs[i].len + chunk - 1) / chunk;
+        // A step's new row is attended apart by the last split's block, so
+        // the splits cover the cached rows (at least one split).
+        const uint32_t cached = seqs[i].len - (seqs[i].k_new != nullptr ? 1u : 0u);
+        table[i].n_splits = std::max(1u, (cached + chunk - 1) / chunk);
         table[i].merge0 = merge_blocks;
         splits += table[i].n_splits;
         if (table[i].n_splits > 1) {

@@ -37,9 +37,14 @@
 // independent 16-byte loads. Each output sums its
 // splits in a fixed order, so results are deterministic.
 //
-// A single-token step passes its new K, V row (k_new, v_new): the block whose
-// split ends at that position rounds it to binary16, attends it from
-// registers and stores it into the cache, so no separate append launch.
+// A single-token step passes its new K, V row (k_new, v_new). The waves'
+// steps cover the cached rows only; the block of the last split also rounds
+// the new row to binary16, stores it into the cache and attends it as a
+// fifth partial of its 4-wave merge (its score computed while the K, V loads
+// are in flight), so there is no separate append launch and the row never
+// makes a split of its own: config 2's 4096 cached rows are 32 splits per KV
+// head, 256 blocks, one per CU. (As its own one-row split the grid was 264
+// blocks, and the 8 CUs holding two blocks finished 1-1.5 us after the rest.)
 
 #include "kernels.hpp"
 
@@ -100,8 +105,11 @@ inline __host__ __device__ uint32_t q_lds_bytes(uint32_t group, uint32_t hd) {
 inline __host__ __device__ uint32_t new_lds_bytes(uint32_t hd) {
     return (2 * hd * 4 + 15) / 16 * 16;
 }
+// (max, sum) slots: 4 waves and the new row, 16 heads each; then the 4
+// waves' parts of the new row's scores, 16 heads each.
+constexpr uint32_t decode_ml_floats = 5 * 16 * 2 + 4 * 16;
 inline __host__ __device__ uint32_t rope_lds_offset(uint32_t group, uint32_t hd) {
-    return q_lds_bytes(group, hd) + new_lds_bytes(hd) + (4 * 16 * 2 + 4 * group * (hd + 4)) * 4;
+    return q_lds_bytes(group, hd) + new_lds_bytes(hd) + (decode_ml_floats + 4 * group * (hd + 4)) * 4;
 }
 inline std::size_t decode_lds_bytes(uint32_t group, uint32_t hd) {
     return rope_lds_offset(group, hd) + std::size_t{hd} * sizeof(float) + 1024 + rope_max_pairs * sizeof(float);
@@ -158,14 +166,16 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     const decode_seq& s = T::seq(a, si);
     const uint32_t split = s.n_splits - 1 - (sb - s.block0);
     const std::size_t slot = static_cast<std::size_t>(s.block0 + split) * p.n_kv + g;
+    // The waves attend the split's cached rows [t_begin, t_end); a step's
+    // new row (position len - 1, from k_new / v_new) is not among them: the
+    // last split's block attends it apart (new_here).
+    const uint32_t cached = s.len - (s.k_new != nullptr ? 1u : 0u);
     const uint32_t t_begin = split * p.chunk;
-    const uint32_t t_end = min(s.len, t_begin + p.chunk);
+    const uint32_t t_end = min(cached, t_begin + p.chunk);
     const uint32_t h0 = g * group;
     const float c = p.scale_log2e;
-    // The step's new row (position len-1) is in this block's split: take it
-    // from k_new / v_new, rounded to binary16, and store it into the cache.
     const uint32_t new_t = s.len - 1;
-    const bool new_here = s.k_new != nullptr && t_end == s.len;
+    const bool new_here = s.k_new != nullptr && split == s.n_splits - 1;
     const bool kv_f16 = !ROPE && p.kv_dtype == 1;  // a fused RoPE step takes f32 rows
 
     // Every K, V load below is unconditional, so a wave issues all of them
@@ -188,6 +198,27 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // same way (K then V, as given), for the step that appends it.
     char* new_lds = lds_bytes + q_lds_bytes(group, hd);
     const uint32_t new_bytes = hd * (kv_f16 ? 2 : 4);
+    // Dims d .. d + 7 (K) or d .. d + 3 (V) of the new row from its LDS
+    // copy, rounded to binary16 as the cache stores them; d is a multiple of
+    // 8 (4), so each is one or two vector reads.
+    const auto new_k8 = [&](uint32_t d) -> h8 {
+        if (kv_f16) {
+            return *reinterpret_cast<const h8*>(new_lds + 2 * d);
+        }
+        const f4 lo = *reinterpret_cast<const f4*>(new_lds + 4 * d);
+        const f4 hi = *reinterpret_cast<const f4*>(new_lds + 4 * d + 16);
+        return h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]), to_h(hi[0]), to_h(hi[1]), to_h(hi[2]), to_h(hi[3])};
+    };
+    const auto new_v4 = [&](uint32_t d) -> f4 {
+        if (kv_f16) {
+            const h4 x = *reinterpret_cast<const h4*>(new_lds + new_bytes + 2 * d);
+            return f4{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
+                      static_cast<float>(x[3])};
+        }
+        const f4 x = *reinterpret_cast<const f4*>(new_lds + new_bytes + 4 * d);
+        return f4{static_cast<float>(to_h(x[0])), static_cast<float>(to_h(x[1])), static_cast<float>(to_h(x[2])),
+                  static_cast<float>(to_h(x[3]))};
+    };
     if (new_here) {
         const std::size_t row_off = static_cast<std::size_t>(g) * new_bytes;
         for (uint32_t c0 = 1024 * w; c0 < 2 * new_bytes; c0 += 4096) {
@@ -203,19 +234,15 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // tb + 8G + 4e + i. V^T rows: lane (G, r) of tile n holds dim 16n + r at
     // positions tb + 8G + [0, 8). Both through buffer resources based at the
     // split: K past the split and dims past the head read as zeros.
-    _Float16* kbase = s.k + g * hd + 8 * G;
     const uint32_t row2 = p.row * 2;
     const uint32_t vstride2 = s.ctx_stride * 2;
-    // The new row's own cache slot is not read (the step overwrites it), nor
-    // are V columns that start at or past it or the split end: those lanes
-    // take zeros and send no request, so a split holding only the new row
-    // waits for no memory. k_rows counts the rows read. K leaves the rest out
-    // through the resource's limit; a V column offset moved past the limit
-    // may wrap into the buffer, which reads valid memory whose values the
-    // step then replaces or zeroes.
+    // k_rows counts the split's rows. K past them reads zeros through the
+    // resource's limit; V columns that start at or past them take an
+    // out-of-range offset (zeros, no request). The new row's cache slot is
+    // never read: the step writes it.
     // (readfirstlane: without it the batched kernel cannot tell the limit is
     // uniform and wraps every K load in a loop over lanes.)
-    const uint32_t k_rows = __builtin_amdgcn_readfirstlane(min(t_end, s.len - (s.k_new != nullptr ? 1u : 0u)) - t_begin);
+    const uint32_t k_rows = __builtin_amdgcn_readfirstlane(t_end - t_begin);
     const rsrc k_res = make_rsrc(s.k + static_cast<std::size_t>(t_begin) * p.row + g * hd,
                                  k_rows ? k_rows * row2 - g * hd * 2 : 0u);
     const rsrc v_res = make_rsrc(s.vt + static_cast<std::size_t>(g) * hd * s.ctx_stride + t_begin,
@@ -319,59 +346,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         }
     };
 
-    // The parts of one 32-position step of the wave on loaded K, V.
-    // inject_new: kv_append (S/kernels/attention.hpp:165-175) of the step's
-    // new row, from its LDS copy, into this step's operands and the cache.
-    const auto inject_new = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
-        const uint32_t tv = tb + 8 * G;
-        if (new_here && tb + decode_positions_per_wave > new_t) {
-            // kv_append (S/kernels/attention.hpp:165-175) of the new row, from
-            // its LDS copy: into this step's operands and into the cache.
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const uint32_t t = tb + 8 * (r >> 2) + 4 * e + (r & 3);
-                if (t == new_t) {
-                    _Float16* kp = kbase + static_cast<std::size_t>(t) * p.row;
-#pragma unroll
-                    for (int st = 0; st < NS; ++st) {
-                        const uint32_t d0 = 8 * G + 32 * st;
-                        if (d0 < hd) {
-                            if (kv_f16) {
-                                kr[e][st] = *reinterpret_cast<const u4*>(new_lds + 2 * d0);
-                            } else {
-                                const f4 lo = *reinterpret_cast<const f4*>(new_lds + 4 * d0);
-                                const f4 hi = *reinterpret_cast<const f4*>(new_lds + 4 * d0 + 16);
-                                kr[e][st] = as_u4(h8{to_h(lo[0]), to_h(lo[1]), to_h(lo[2]), to_h(lo[3]),
-                                                     to_h(hi[0]), to_h(hi[1]), to_h(hi[2]), to_h(hi[3])});
-                            }
-                            store16(kp + 32 * st, kr[e][st]);
-                        }
-                    }
-                }
-            }
-            if (tv <= new_t && new_t < tv + 8) {
-                const uint32_t j = new_t - tv;
-#pragma unroll
-                for (int n = 0; n < NT; ++n) {
-                    const uint32_t dim = 16 * n + r;
-                    if (dim < hd) {
-                        const _Float16 x =
-                            kv_f16 ? *reinterpret_cast<const _Float16*>(new_lds + new_bytes + 2 * dim)
-                                   : to_h(*reinterpret_cast<const float*>(new_lds + new_bytes + 4 * dim));
-                        h8 v = as_h8(vr[n]);
-#pragma unroll
-                        for (uint32_t jj = 0; jj < 8; ++jj) {
-                            if (jj == j) {
-                                v[jj] = x;
-                            }
-                        }
-                        vr[n] = as_u4(v);
-                        s.vt[static_cast<std::size_t>(g * hd + dim) * s.ctx_stride + new_t] = x;
-                    }
-                }
-            }
-        }
-    };
     // scores: raw q.k of head r at positions tv + 4e + i in sc[e][i], -inf
     // past the split end; returns their max over the wave's 32 positions.
     const auto scores = [&](uint32_t tv, u4 (&kr)[2][NS], f4 (&sc)[2]) {
@@ -425,7 +399,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // running sum and O rescaled when the max grows.
     const auto step = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
         const uint32_t tv = tb + 8 * G;
-        inject_new(tb, kr, vr);
         f4 sc[2];
         const float bm = scores(tv, kr, sc);
         const float m_new = fmaxf(m_run, bm);
@@ -484,6 +457,38 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     }
     convert_q(ROPE || tb < t_end);
     float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));
+    // The new row, from its LDS copy (rotated there by a fused RoPE step),
+    // while the K, V loads are in flight: wave w takes the
+    // part of its raw score q.k over the dims of k-step w (mod 4) for every
+    // head of the group, and the merge adds the 4 parts in wave order. As a
+    // split of one row it has p = 1 at its own max: the fifth (max, sum)
+    // slot is (score, 1). (One wave taking the whole score held its own
+    // step, and the block, back by 0.5 us.)
+    float* lds_snew = lds_ml + 5 * 16 * 2;
+    const auto new_score = [&](uint32_t h) {
+        return ((lds_snew[h] + lds_snew[16 + h]) + lds_snew[32 + h]) + lds_snew[48 + h];
+    };
+    if (new_here) {
+        // Lane (G, r) holds head r's q at dims 32 st + 8 G + [0, 8): the
+        // products of two binary16 values are exact in f32, summed in f32
+        // over the lane's dims, then over the 4 lane groups.
+        float part = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const uint32_t d0 = 8 * G + 32 * st;
+            if (st % 4 == w && d0 < hd) {
+                const h8 kn = new_k8(d0);
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) {
+                    part = fmaf(static_cast<float>(qv[st][j]), static_cast<float>(kn[j]), part);
+                }
+            }
+        }
+        part = sum32(sum16(part));
+        if (G == 0) {
+            lds_snew[16 * w + r] = part;
+        }
+    }
     // A sequence of at most 128 rows is one split in which every wave takes
     // at most one step. Its softmax is then taken whole, as attend_group
     // takes it (S/kernels/attention.hpp:222-227): max and sum over all the
@@ -499,7 +504,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         f4 sc[2];
         float bm = -INFINITY;
         if (have) {
-            inject_new(tb, kr, vr);
             bm = scores(tv, kr, sc);
         } else {
             sc[0] = sc[1] = f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
@@ -513,6 +517,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         for (int v = 1; v < 4; ++v) {
             mx = fmaxf(mx, lds_ml[(v * 16 + r) * 2]);
         }
+        const float s_new = new_here ? new_score(r) : -INFINITY;
+        mx = fmaxf(mx, s_new);
         const float m_use = mx == -INFINITY ? 0.0f : mx;
         float ex[8];
         float es = 0.0f;
@@ -534,7 +540,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         for (int v = 0; v < 4; ++v) {
             total += lds_ml[(v * 16 + r) * 2 + 1];
         }
+        const float ex_new = fast_exp2((s_new - m_use) * c);  // 0 without a new row
+        total += ex_new;
         const float inv = 1.0f / total;
+        // The new row's normalised p, rounded as the others, for the merge
+        // below (no wave reads this slot before the barrier there).
+        if (new_here && w == 0 && G == 0 && static_cast<uint32_t>(r) < group) {
+            lds_ml[(64 + r) * 2 + 1] = static_cast<float>(to_h(ex_new * inv));
+        }
         h8 pa;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -561,7 +574,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // waves hold normalised parts of one sum (and other waves may still be
     // reading the (max, sum) slots), so they write O only.
     const uint32_t orow = hd + 4;
-    float* lds_o = lds_ml + 4 * 16 * 2;
+    float* lds_o = lds_ml + decode_ml_floats;
     if (G == 0 && !whole) {
         lds_ml[(w * 16 + r) * 2] = m_run;
         lds_ml[(w * 16 + r) * 2 + 1] = l_run;
@@ -583,27 +596,53 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // the output for a sequence of one split, else this split's partial,
     // which the merge kernel reads after the kernel boundary.
     const uint32_t nout = group * hd;
+    // The new row into the cache as binary16 (kv_append, S/kernels/
+    // attention.hpp:165-175), by the threads the merge below leaves idle
+    // (the last wave when it has work for every thread): K 16 bytes per
+    // lane, V^T one binary16 per dim, a column. Here its scattered stores
+    // delay no load or product of the block.
+    if (new_here) {
+        const uint32_t t0 = nout / 4 < 256 - 64 ? (nout / 4 + 63) / 64 * 64 : 192;
+        for (uint32_t i = tid - t0; tid >= t0 && i < hd / 4; i += 256 - t0) {
+            const uint32_t d = 4 * i;
+            if (d % 8 == 0) {
+                store16(s.k + static_cast<std::size_t>(new_t) * p.row + g * hd + d, as_u4(new_k8(d)));
+            }
+            const f4 x = new_v4(d);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s.vt[static_cast<std::size_t>(g * hd + d + j) * s.ctx_stride + new_t] = static_cast<_Float16>(x[j]);
+            }
+        }
+    }
     float* part_o = p.part + slot * nout;
     float* part_ml = p.part + static_cast<std::size_t>(p.total_slots) * nout + slot * group * 2;
     for (uint32_t e = 4 * tid; e < nout; e += 4 * 256) {
         const uint32_t h = e / hd;
         const uint32_t d = e % hd;
+        // The new row's V at dims d .. d + 3 (binary16 values).
+        const f4 vnew = new_here ? new_v4(d) : f4{0.0f, 0.0f, 0.0f, 0.0f};
         if (whole) {
             f4 acc = *reinterpret_cast<const f4*>(lds_o + h * orow + d);
 #pragma unroll
             for (int v = 1; v < 4; ++v) {
                 acc += *reinterpret_cast<const f4*>(lds_o + (v * group + h) * orow + d);
             }
+            if (new_here) {
+                acc += lds_ml[(64 + h) * 2 + 1] * vnew;
+            }
             *reinterpret_cast<f4*>(s.out + static_cast<std::size_t>(h0) * hd + e) = acc;
             continue;
         }
-        float mw[4];
+        float mw[5];
         float mx = -INFINITY;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             mw[v] = lds_ml[(v * 16 + h) * 2];
             mx = fmaxf(mx, mw[v]);
         }
+        mw[4] = new_here ? new_score(h) : -INFINITY;
+        mx = fmaxf(mx, mw[4]);
         float sum = 0.0f;
         f4 acc{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -611,6 +650,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
             const float f = fast_exp2((mw[v] - mx) * c);  // 0 for a wave with no positions
             sum += lds_ml[(v * 16 + h) * 2 + 1] * f;
             acc += f * *reinterpret_cast<const f4*>(lds_o + (v * group + h) * orow + d);
+        }
+        if (new_here) {
+            const float f = fast_exp2((mw[4] - mx) * c);
+            sum += f;
+            acc += f * vnew;
         }
         if (s.n_splits == 1) {
             *reinterpret_cast<f4*>(s.out + static_cast<std::size_t>(h0) * hd + e) = acc / sum;

@@ -144,11 +144,20 @@ def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int,
     det = {"eager_ms_per_step": eager_ms, "wall_ms_per_step": wall_ms, "kernel_ms_median": float(np.median(kern)),
            "timing": "HIP-graph launch of the timed steps" if graph else "steps called one by one"}
     if graph:
-        with capi.HipGraph(arena, lambda: [step(warmup + i) for i in range(steps)]) as hg:
+        warm = max(warmup, 1)  # (a graph needs a node: with W = 0 one step leads)
+        with capi.HipGraph(arena, lambda: [step(i) for i in range(warm)]) as hw, \
+                capi.HipGraph(arena, lambda: [step(warmup + i) for i in range(steps)]) as hg:
+            hw.upload()
             hg.upload()
-            for i in range(warmup):
-                step(i)
+            hw.launch()
             arena.sync()
+            # The warm-up steps run again right ahead of the start event, as a
+            # graph: the GPU is busy with them while this process queues the
+            # event and the timed graph, so the timed region holds the K steps
+            # and not the host's launch latency (about 14 us before the first
+            # kernel otherwise, 0.7 us per step at K = 20). The start event
+            # is stream-ordered after the last warm-up kernel.
+            hw.launch()
             hip.record(t0, stream)
             hg.launch()
             hip.record(t1, stream)
@@ -262,8 +271,73 @@ def bench_prefill(hip: Hip, cfg: wl.Prefill, reps: int):
         check(L.syn_hip_attention(arena.handle, ctypes.byref(d)))
     hip.record(t1, stream)
     op_ms = hip.ms(t0, t1) / reps
+    # The append alone is shorter than a host call: replayed from a graph.
+    def appends():
+        for i in range(reps):
+            check(L.syn_hip_kv_append(arena.handle, ctypes.byref(cache), d.k_offset, d.v_offset, cfg.n, 0, SYN_F16))
+
+    arena.sync()
+    with capi.HipGraph(arena, appends) as hg:
+        hg.upload()
+        hg.launch()
+        t0, t1 = hip.events(2)
+        hip.record(t0, stream)
+        hg.launch()
+        hip.record(t1, stream)
+        append_ms = hip.ms(t0, t1) / reps
+        arena.sync()
     arena.close()
-    return kern_ms, op_ms
+    return kern_ms, op_ms, append_ms
+
+
+def bench_prefill_rope(hip: Hip, cfg: wl.Prefill, reps: int):
+    """Config 3 with Llama 3's RoPE on the run's q and k rows (f32, as op_rope
+    takes them): one syn_hip_attention_rope call (the rotating append, then
+    the prefill kernel: 2 launches) against the separate calls (rope q, rope
+    k, then syn_hip_attention's append and prefill: 4 launches)."""
+    qsz = cfg.n_heads * cfg.head_dim
+    row = cfg.n_kv * cfg.head_dim
+    arena = Arena(capi.kv_state_bytes(cfg.n, cfg.n_kv, cfg.head_dim) + cfg.n * (qsz * 12 + row * 16) + (8 << 20))
+    q, k, v = wl.prefill_inputs(cfg)
+    cache = capi.kv_state(arena, cfg.n, cfg.n_kv, cfg.head_dim)
+    q_off, k_off, v_off = (arena.put(np.asarray(x, dtype=np.float32)) for x in (q, k, v))
+    qr, kr, out = arena.alloc(cfg.n * qsz * 4), arena.alloc(cfg.n * row * 4), arena.alloc(cfg.n * qsz * 4)
+    theta_scale = float(np.float32(cfg.theta) ** np.float32(-2.0 / cfg.head_dim))
+    rope = dict(freq_factors_offset=capi.NO_OFFSET, theta_scale=theta_scale, mode=0, freq_scale=1.0,
+                ext_factor=0.0, attn_factor=1.0, corr_low=0.0, corr_high=0.0)
+    d = AttnDesc(cache=cache, q_offset=q_off, k_offset=k_off, v_offset=v_off, out_offset=out, scratch_offset=0,
+                 scratch_bytes=0, n_heads=cfg.n_heads, pos=0, n=cfg.n, scale=cfg.scale, q_dtype=SYN_F32,
+                 kv_dtype=SYN_F32)
+    r = capi.AttnRopeDesc(q_out_offset=qr, k_out_offset=kr, temp_scale=0.0, temp_floor_len=0, **rope)
+    rq = capi.RopeDesc(in_offset=q_off, out_offset=qr, n=cfg.n, size=qsz, head_dim=cfg.head_dim, pos=0, **rope)
+    rk = capi.RopeDesc(in_offset=k_off, out_offset=kr, n=cfg.n, size=row, head_dim=cfg.head_dim, pos=0, **rope)
+    d2 = AttnDesc(cache=cache, q_offset=qr, k_offset=kr, v_offset=v_off, out_offset=out, scratch_offset=0,
+                  scratch_bytes=0, n_heads=cfg.n_heads, pos=0, n=cfg.n, scale=cfg.scale, q_dtype=SYN_F32,
+                  kv_dtype=SYN_F32)
+    L = lib()
+
+    def run_fused():
+        check(L.syn_hip_attention_rope(arena.handle, ctypes.byref(d), ctypes.byref(r)))
+
+    def run_separate():
+        check(L.syn_hip_rope(arena.handle, ctypes.byref(rq)))
+        check(L.syn_hip_rope(arena.handle, ctypes.byref(rk)))
+        check(L.syn_hip_attention(arena.handle, ctypes.byref(d2)))
+
+    result = {}
+    for name, fn in (("fused_us", run_fused), ("separate_us", run_separate)):
+        fn()
+        arena.sync()
+        t0, t1 = hip.events(2)
+        hip.record(t0, arena.stream)
+        for _ in range(reps):
+            fn()
+        hip.record(t1, arena.stream)
+        result[name] = round(hip.ms(t0, t1) / reps * 1e3, 2)
+    assert np.all(np.isfinite(arena.download(out, (cfg.n, qsz), np.float32)))
+    arena.close()
+    result.update({"launches_fused": 2, "launches_separate": 4, "rows": "f32"})
+    return result
 
 
 def bench_ragged(hip: Hip, cfg: wl.Ragged, reps: int):
@@ -549,13 +623,19 @@ def main() -> int:
     if only in (None, "prefill"):
         p = wl.C3
         log(f"prefill {p.name}")
-        kms, op_ms = bench_prefill(hip, p, 50)
+        kms, op_ms, app_ms = bench_prefill(hip, p, 50)
         tf = p.flops() / (kms * 1e-3) / 1e12
+        app_bytes = 2 * p.n * p.n_kv * p.head_dim * (2 + 2)  # K and V: binary16 rows in, cache rows out
         extra["prefill"] = {"kernel_us": round(kms * 1e3, 2), "tflops": round(tf, 1),
                             "frac_of_f16_peak": round(tf / MFMA_F16_PEAK_TFS, 4),
                             "op_us_with_append": round(op_ms * 1e3, 2),
+                            "append_us": round(app_ms * 1e3, 2),
+                            "append_gbs": round(app_bytes / (app_ms * 1e-3) / 1e9, 1),
+                            "append_frac_of_hbm": round(app_bytes / (app_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                             "tokens_per_s": round(p.n / (op_ms * 1e-3), 0), "flops": p.flops()}
-        log(f"prefill: {kms * 1e3:.1f} us, {tf:.0f} TFLOP/s")
+        extra["prefill_rope"] = bench_prefill_rope(hip, p, 20)
+        log(f"prefill: {kms * 1e3:.1f} us, {tf:.0f} TFLOP/s; append {app_ms * 1e3:.2f} us; "
+            f"with RoPE {extra['prefill_rope']}")
     if only in (None, "ragged"):
         r = wl.C4
         log(f"ragged {r.name}")

@@ -235,13 +235,18 @@ int syn_hip_attn_temperature(syn_arena* arena, const syn_temperature_desc* desc)
  * rows before RoPE, f32. A single-token step that the split-KV decode
  * kernel takes is that one kernel: it rotates q and the new K row in LDS
  * with syn_hip_rope's arithmetic, multiplies q by the temperature, stores
- * the rotated K row into the cache, and writes no rotated rows -- equal, bit
- * for bit, to the separate calls. Any other run makes the separate calls:
- * rotated (and scaled) q rows to q_out_offset, rotated k rows to
- * k_out_offset, then syn_hip_attention on them. */
+ * the rotated K row into the cache, and writes no rotated rows. Any other
+ * run (several tokens, or head sizes that kernel does not take) is two
+ * launches: one rotates q (and multiplies it by the temperature) into
+ * binary16 rows at q_out_offset, rotates the K rows into the cache and
+ * appends the V rows; then the attention kernel reads those q rows. Both
+ * are equal, bit for bit, to the separate calls (binary16 is the rounding
+ * the attention kernels give f32 q). q_out must not overlap the q, k or v
+ * rows. */
 typedef struct syn_attn_rope_desc {
-    uint64_t q_out_offset;        /* n rows of n_heads*head_dim f32 (runs that do not fuse) */
-    uint64_t k_out_offset;        /* n rows of n_kv_heads*head_dim f32 (likewise) */
+    uint64_t q_out_offset;        /* room for n rows of n_heads*head_dim f32, 16-byte aligned; runs write
+                                     binary16 rows into its first half, the single-token step nothing */
+    uint64_t k_out_offset;        /* unused (rotated K rows go straight to the cache) */
     uint64_t freq_factors_offset; /* head_dim/2 f32 (16-byte aligned), or UINT64_MAX for none */
     float theta_scale;
     uint32_t mode;                /* 0 normal, 1 neox */

@@ -191,6 +191,9 @@ class HipGraph:
         finally:
             _hip_ok(rt.hipStreamEndCapture(self.stream, ctypes.byref(graph)), "hipStreamEndCapture")
         try:
+            count = ctypes.c_size_t(0)
+            _hip_ok(rt.hipGraphGetNodes(graph, None, ctypes.byref(count)), "hipGraphGetNodes")
+            self.nodes = count.value  # the captured launches (and any other recorded operations)
             _hip_ok(rt.hipGraphInstantiate(ctypes.byref(self._exec), graph, None, None, 0), "hipGraphInstantiate")
         finally:
             rt.hipGraphDestroy(graph)
@@ -233,6 +236,7 @@ def _hip_runtime() -> ctypes.CDLL:
                            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
                            "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, ctypes.c_size_t],
                            "hipGraphLaunch": [vp, vp], "hipGraphUpload": [vp, vp], "hipGraphDestroy": [vp],
+                           "hipGraphGetNodes": [vp, ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_size_t)],
                            "hipGraphExecDestroy": [vp]}.items():
             getattr(rt, name).argtypes = args
             getattr(rt, name).restype = ctypes.c_int

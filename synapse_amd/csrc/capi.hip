@@ -660,48 +660,52 @@ int syn_hip_attention_rope(syn_arena* a, const syn_attn_desc* d, const syn_attn_
         rp.temp_floor_len = r->temp_floor_len;
         return attend_checked(a, d, true, nullptr, &rp);
     }
-    // The separate ops, into the caller's rows.
-    syn_rope_desc rd{};
-    rd.freq_factors_offset = r->freq_factors_offset;
-    rd.n = d->n;
-    rd.head_dim = c.head_dim;
-    rd.pos = d->pos;
-    rd.theta_scale = r->theta_scale;
-    rd.mode = r->mode;
-    rd.freq_scale = r->freq_scale;
-    rd.ext_factor = r->ext_factor;
-    rd.attn_factor = r->attn_factor;
-    rd.corr_low = r->corr_low;
-    rd.corr_high = r->corr_high;
-    rd.in_offset = d->q_offset;
-    rd.out_offset = r->q_out_offset;
-    rd.size = d->n_heads * c.head_dim;
-    if (int e = syn_hip_rope(a, &rd)) {
+    // A run (or a head size the split-KV kernel does not take): one launch
+    // rotates q (times the temperature) into binary16 rows at q_out_offset,
+    // rotates and appends the K rows and appends the V rows; then the
+    // attention kernel reads those q rows. binary16 is the rounding every
+    // attention kernel applies to f32 q, so this equals the separate calls.
+    const uint64_t q_bytes = uint64_t{d->n} * d->n_heads * c.head_dim * 4;
+    const uint64_t kv_bytes = uint64_t{d->n} * c.n_kv_heads * c.head_dim * 4;
+    if (int e = check_range(a, r->q_out_offset, q_bytes, 16, "attention_rope q_out")) {
         return e;
     }
-    if (r->temp_floor_len != 0) {
-        syn_temperature_desc td{};
-        td.in_offset = r->q_out_offset;
-        td.out_offset = r->q_out_offset;
-        td.n = d->n;
-        td.size = rd.size;
-        td.pos = d->pos;
-        td.floor_len = r->temp_floor_len;
-        td.scale = r->temp_scale;
-        if (int e = syn_hip_attn_temperature(a, &td)) {
-            return e;
-        }
+    const auto overlap = [](uint64_t p, uint64_t pn, uint64_t q, uint64_t qn) { return p < q + qn && q < p + pn; };
+    if (overlap(r->q_out_offset, q_bytes, d->q_offset, q_bytes) ||
+        overlap(r->q_out_offset, q_bytes, d->k_offset, kv_bytes) ||
+        overlap(r->q_out_offset, q_bytes, d->v_offset, kv_bytes)) {
+        return fail(SYN_HIP_EINVAL, "attention_rope: q_out overlaps the q, k or v rows");
     }
-    rd.in_offset = d->k_offset;
-    rd.out_offset = r->k_out_offset;
-    rd.size = c.n_kv_heads * c.head_dim;
-    if (int e = syn_hip_rope(a, &rd)) {
+    syn::append_run_args ar{};
+    ar.k_rows = a->base + d->k_offset;
+    ar.v_rows = a->base + d->v_offset;
+    ar.k_cache = reinterpret_cast<_Float16*>(a->base + c.k_offset);
+    ar.vt_cache = reinterpret_cast<_Float16*>(a->base + c.v_offset);
+    ar.row = c.n_kv_heads * c.head_dim;
+    ar.hd = c.head_dim;
+    ar.n = d->n;
+    ar.pos0 = d->pos;
+    ar.ctx_stride = c.ctx_stride;
+    ar.q = reinterpret_cast<const float*>(a->base + d->q_offset);
+    ar.q16 = reinterpret_cast<_Float16*>(a->base + r->q_out_offset);
+    ar.q_size = d->n_heads * c.head_dim;
+    ar.r.freq_factors = ff;
+    ar.r.mode = r->mode;
+    ar.r.theta_scale = r->theta_scale;
+    ar.r.freq_scale = r->freq_scale;
+    ar.r.ext_factor = r->ext_factor;
+    ar.r.attn_factor = r->attn_factor;
+    ar.r.corr_low = r->corr_low;
+    ar.r.corr_high = r->corr_high;
+    ar.r.temp_scale = r->temp_scale;
+    ar.r.temp_floor_len = r->temp_floor_len;
+    if (int e = hip_status(syn::launch_append_run(ar, 0, true, a->stream), "rope append launch")) {
         return e;
     }
     syn_attn_desc rotated = *d;
     rotated.q_offset = r->q_out_offset;
-    rotated.k_offset = r->k_out_offset;
-    return syn_hip_attention(a, &rotated);
+    rotated.q_dtype = SYN_F16;
+    return attend_checked(a, &rotated, false);
 }
 
 uint64_t syn_hip_attention_noalloc_scratch_limit(void) {

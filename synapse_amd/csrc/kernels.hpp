@@ -184,6 +184,27 @@ __device__ inline float attn_temperature(uint32_t pos, float scale, uint32_t flo
     return static_cast<float>(log(static_cast<double>(q) + 1.0) * static_cast<double>(scale) + 1.0);
 }
 
+// A run's append (kv_append.hip): K rows to the cache, V rows to V^T, both
+// rounded to binary16 (rows f32 or binary16). With RoPE (f32 rows only) the
+// run's q and K rows are rotated on the way, as op_rope rotates them, and q
+// is multiplied by the attention temperature (none when
+// r.temp_floor_len is 0): q goes to q16 as binary16 rows, K to the cache.
+struct append_run_args {
+    const void* k_rows;      // n rows of `row` elements
+    const void* v_rows;
+    _Float16* k_cache;       // K rows of the cache (row 0)
+    _Float16* vt_cache;      // V^T of the cache
+    uint32_t row, hd, n, pos0, ctx_stride;
+    const float* q;          // RoPE: n rows of q_size f32
+    _Float16* q16;           // RoPE: n rows of q_size binary16 out
+    uint32_t q_size;
+    rope_params r;           // RoPE parameters and the temperature
+    // set by launch_append_run
+    uint32_t v_tiles, v_feat_tiles;
+    bool vec;                // rows 16-byte aligned: vector loads
+};
+hipError_t launch_append_run(append_run_args a, uint32_t dtype, bool rope, hipStream_t stream);
+
 // Scratch floats one split contributes: (max, sum, output) for each head.
 inline std::size_t decode_split_floats(uint32_t group, uint32_t hd) {
     return static_cast<std::size_t>(group) * (hd + 2);

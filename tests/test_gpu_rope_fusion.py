@@ -122,15 +122,49 @@ def test_fused_temperature_equals_separate_over_positions(arena, temp):
         assert np.array_equal(cache_f[0], cache_s[0]) and np.array_equal(cache_f[1], cache_s[1]), ctx
 
 
-@pytest.mark.parametrize("n_heads,n_kv,hd,ctx,n", [(32, 8, 128, 100, 37), (4, 2, 12, 20, 1), (6, 2, 20, 0, 5)])
-def test_unfused_runs_make_the_separate_calls(arena, n_heads, n_kv, hd, ctx, n):
+@pytest.mark.parametrize("n_heads,n_kv,hd,ctx,n,mode,yarn", [
+    (32, 8, 128, 100, 37, 0, False),   # a run after 100 cached rows
+    (32, 8, 128, 0, 2048, 0, False),   # config 3's run
+    (28, 4, 128, 61, 200, 1, True),    # neox pairs, YaRN
+    (4, 2, 12, 20, 1, 0, False),       # head size the split-KV kernel does not take
+    (6, 2, 20, 0, 5, 1, False),
+])
+def test_runs_fuse_into_two_launches(arena, n_heads, n_kv, hd, ctx, n, mode, yarn):
     """Several tokens (prefill) and head sizes the split-KV kernel does not
-    take: the same results, and the rotated rows where the descriptor says."""
-    got, want, cache_f, cache_s, rotated, want_rot = _layer(arena, n_heads, n_kv, hd, ctx, n, 0, False, True,
+    take: the rotation, temperature and append in one launch, then the
+    attention kernel. Outputs and cache rows equal the separate calls; q_out
+    holds the rotated, scaled q rows as binary16 (the separate calls' f32
+    rows rounded to nearest even); k_out is not written."""
+    got, want, cache_f, cache_s, rotated, want_rot = _layer(arena, n_heads, n_kv, hd, ctx, n, mode, yarn, True,
                                                             (0.25, 4), seed=n + hd)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     assert np.array_equal(cache_f[0], cache_s[0]) and np.array_equal(cache_f[1], cache_s[1])
-    assert np.array_equal(rotated[0], want_rot[0]) and np.array_equal(rotated[1], want_rot[1])
+    q16 = rotated[0].reshape(-1).view(np.uint16)[:want_rot[0].size].reshape(want_rot[0].shape)
+    assert np.array_equal(q16, want_rot[0].astype(np.float16).view(np.uint16))
+    assert not rotated[1].any()
+
+
+@pytest.mark.parametrize("n,launches", [(2048, 2), (37, 2), (1, 1)])
+def test_fused_call_launch_count(arena, n, launches):
+    """Captured into a HIP graph, syn_hip_attention_rope records two kernel
+    launches for a run of config 3's shape and one for a decode step (the
+    separate calls: rope q, rope k, the append, then attention)."""
+    n_heads, n_kv, hd, ctx = 32, 8, 128, 64
+    g = wl.rng(n)
+    row, qsz = n_kv * hd, n_heads * hd
+    mark = arena.top
+    cache = capi.kv_state(arena, ctx + n, n_kv, hd)
+    q_off, k_off, v_off = (put_rows(arena, wl.normal(g, (n, m)), SYN_F32) for m in (qsz, row, row))
+    qr, kr, out = arena.alloc(n * qsz * 4), arena.alloc(n * row * 4), arena.alloc(n * qsz * 4)
+    scratch = scratch_for(arena, n_heads, n_kv, hd, ctx + n)
+    d = attn_desc(cache, q_off, k_off, v_off, out, scratch, n_heads, ctx, n, float(1 / np.sqrt(hd)))
+    r = AttnRopeDesc(q_out_offset=qr, k_out_offset=kr, **_rope_params(hd, 0, False, capi.NO_OFFSET))
+    arena.sync()
+    with capi.HipGraph(arena, lambda: check(lib().syn_hip_attention_rope(arena.handle, ctypes.byref(d),
+                                                                         ctypes.byref(r)))) as hg:
+        nodes = hg.nodes
+    arena.top = mark
+    assert nodes == launches
 
 
 def test_fused_step_rejects_f16_rows(arena):

@@ -3,9 +3,12 @@ C++ host tests) in-tree.
 
     python -m synapse_amd.build            # library + oracle + host tests
     python -m synapse_amd.build --lib      # library only
+    python -m synapse_amd.build --stamps   # the decode phase-stamp timing build
 
 Outputs (git-ignored, but shipped to the GPU box with the tree):
     synapse_amd/libsynapse_hip.so          the C ABI of include/synapse_hip.h
+    synapse_amd/libsynapse_hip_stamps.so   the same with decode phase stamps
+                                           (synapse_amd/decode_phases.py reads them)
     oracle/liboracle.so                    CPU oracle (test infrastructure)
     oracle/_ref/libref_half.so             the reference's own binary16 code
     tests/cpp/_bin/*                       C++ host tests
@@ -25,6 +28,7 @@ PKG = ROOT / "synapse_amd"
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libsynapse_hip.so"
+STAMPS_LIB = PKG / "libsynapse_hip_stamps.so"
 HOST_INC = PKG / "host"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -55,23 +59,28 @@ def _run(cmd: list[str], cwd: pathlib.Path | None = None) -> None:
         raise RuntimeError(f"build failed ({' '.join(cmd)}):\n{out}")
 
 
-def build_library() -> pathlib.Path:
-    BUILD.mkdir(exist_ok=True)
+def build_library(stamps: bool = False) -> pathlib.Path:
+    """The library; with stamps, the timing build whose decode kernels record
+    phase timestamps (SYN_DECODE_STAMPS), to its own file."""
+    build = BUILD / "stamps" if stamps else BUILD
+    lib = STAMPS_LIB if stamps else LIB
+    build.mkdir(parents=True, exist_ok=True)
     objs = []
 
     def compile_one(src: str) -> pathlib.Path:
-        obj = BUILD / (pathlib.Path(src).stem + ".o")
-        _run([HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)])
+        obj = build / (pathlib.Path(src).stem + ".o")
+        extra = ["-DSYN_DECODE_STAMPS"] if stamps else []
+        _run([HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), *extra, "-c", str(CSRC / src), "-o", str(obj)])
         return obj
 
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(HIP_SOURCES))) as ex:
         objs = list(ex.map(compile_one, HIP_SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     # -z defs: an unresolved symbol fails the link (a kernel whose host stub
     # the compiler silently dropped would otherwise surface only at load time).
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", str(tmp), *map(str, objs)])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 def build_oracle() -> None:
@@ -115,10 +124,15 @@ def build_host_tests() -> None:
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--lib", action="store_true", help="build the HIP library only")
+    ap.add_argument("--stamps", action="store_true", help="build the decode phase-stamp timing library only")
     args = ap.parse_args(argv)
     if not shutil.which(HIPCC) and not pathlib.Path(HIPCC).exists():
         print(f"hipcc not found at {HIPCC}", file=sys.stderr)
         return 1
+    if args.stamps:
+        build_library(stamps=True)
+        print(f"built {STAMPS_LIB.relative_to(ROOT)}")
+        return 0
     build_library()
     print(f"built {LIB.relative_to(ROOT)}")
     if not args.lib:

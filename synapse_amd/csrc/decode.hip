@@ -50,6 +50,24 @@
 
 namespace syn {
 
+#ifdef SYN_DECODE_STAMPS
+// Timing build only (python -m synapse_amd.build --stamps): every wave of the
+// split kernel's first decode_stamp_blocks blocks keeps s_memrealtime stamps
+// (100 MHz, one clock for the whole device) at decode_stamp_points phase
+// points; every merge block its entry and end. Block 0 of a split launch
+// first copies the previous launch's merge stamps aside, so one read after a
+// run of steps shows a whole step: previous merge, split, merge.
+constexpr uint32_t decode_stamp_blocks = 512;
+constexpr uint32_t decode_stamp_points = 9;
+constexpr uint32_t decode_stamp_merges = 64;
+__device__ unsigned long long decode_stamp_split[decode_stamp_blocks * 4 * decode_stamp_points];
+__device__ unsigned long long decode_stamp_merge[decode_stamp_merges * 2];
+__device__ unsigned long long decode_stamp_prev[decode_stamp_merges * 2];
+#define DECODE_STAMP(k) stamp_[k] = __builtin_amdgcn_s_memrealtime()
+#else
+#define DECODE_STAMP(k) (void)0
+#endif
+
 namespace {
 
 // The sequence a block belongs to: starts[] is non-decreasing, and sequence
@@ -145,6 +163,15 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     constexpr int NS = HDP / 32;   // k-steps of the score product
     constexpr int NT = HDP / 16;   // 16-dim tiles of the output
 
+#ifdef SYN_DECODE_STAMPS
+    unsigned long long stamp_[decode_stamp_points] = {};
+    if (blockIdx.x == 0 && threadIdx.x < 64) {
+        for (uint32_t i = threadIdx.x; i < decode_stamp_merges * 2; i += 64) {
+            decode_stamp_prev[i] = decode_stamp_merge[i];
+        }
+    }
+#endif
+    DECODE_STAMP(0);
     const int tid = threadIdx.x;
     const int w = tid >> 6;
     const int ln = tid & 63;
@@ -169,6 +196,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // The waves attend the split's cached rows [t_begin, t_end); a step's
     // new row (position len - 1, from k_new / v_new) is not among them: the
     // last split's block attends it apart (new_here).
+    // The arguments the K, V loads need, materialised here: the compiler
+    // otherwise fetches them after the q copy below, a second dependent
+    // round trip to the kernel arguments (about half a microsecond) before
+    // any wave's first K, V load.
+    asm volatile("" : : "s"(s.len), "s"(s.n_splits), "s"(s.ctx_stride), "s"(p.scale_log2e));
     const uint32_t cached = s.len - (s.k_new != nullptr ? 1u : 0u);
     const uint32_t t_begin = split * p.chunk;
     const uint32_t t_end = min(cached, t_begin + p.chunk);
@@ -401,6 +433,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         const uint32_t tv = tb + 8 * G;
         f4 sc[2];
         const float bm = scores(tv, kr, sc);
+        DECODE_STAMP(3);
         const float m_new = fmaxf(m_run, bm);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         const float alpha = fast_exp2((m_run - m_use) * c);
@@ -422,7 +455,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         for (int n = 0; n < NT; ++n) {
             o[n] *= alpha;
         }
+        DECODE_STAMP(4);
         accumulate(tv, vr, pa);
+        DECODE_STAMP(5);
     };
 
     // The wave's first K, V loads go out with q's; later steps load their
@@ -448,6 +483,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     if (ROPE || tb < t_end) {
         load_kv(tb, kr, vr);
     }
+    DECODE_STAMP(1);
     if constexpr (ROPE) {
         // The angles need neither q nor the factors: lane 0 of wave 0 runs
         // their chain while the loads are in flight.
@@ -456,6 +492,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         }
     }
     convert_q(ROPE || tb < t_end);
+    DECODE_STAMP(2);
     float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));
     // The new row, from its LDS copy (rotated there by a fused RoPE step),
     // while the K, V loads are in flight: wave w takes the
@@ -590,7 +627,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     }
     // LDS only: the block appending the step's row must not wait here for
     // its scattered cache stores, as __syncthreads() would.
+    DECODE_STAMP(6);
     lds_barrier();
+    DECODE_STAMP(7);
 
     // Every thread combines the waves for 4 consecutive elements of one head:
     // the output for a sequence of one split, else this split's partial,
@@ -666,6 +705,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
             }
         }
     }
+#ifdef SYN_DECODE_STAMPS
+    DECODE_STAMP(8);
+    if (ln == 0 && b < decode_stamp_blocks) {
+        for (uint32_t k = 0; k < decode_stamp_points; ++k) {
+            decode_stamp_split[(b * 4 + w) * decode_stamp_points + k] = stamp_[k];
+        }
+    }
+#endif
 }
 
 // One block per (sequence with splits, query head): out = sum_j w_j O_j with
@@ -680,8 +727,11 @@ template <class A>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const A a) {
     using T = decode_traits<A>;
     const decode_params& p = a.p;
-    __shared__ float wts[decode_max_splits];
-    __shared__ f4 acc_lds[256];
+#ifdef SYN_DECODE_STAMPS
+    unsigned long long stamp_[1];
+    DECODE_STAMP(0);
+    const unsigned long long entry_ = stamp_[0];
+#endif
     const int tid = threadIdx.x;
     const int ln = tid & 63;
     const uint32_t u = blockIdx.x;
@@ -705,88 +755,112 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const A a) {
     const rsrc o_r = make_rsrc(p.part + slot0 * nout + static_cast<std::size_t>(h) * hd, (S - 1) * o_stride + hd * 4);
     const rsrc ml_r = make_rsrc(p.part + static_cast<std::size_t>(p.total_slots) * nout + (slot0 * group + h) * 2,
                                 (S - 1) * ml_stride + 8);
+    // Every argument fetched in the first batch of scalar loads (the
+    // compiler otherwise fetches these after the first loads, a second
+    // dependent round trip).
+    asm volatile("" : : "s"(p.total_slots), "s"(c), "s"(s.out));
 
-    // The head's hd/4 output quads times P parts of the splits fill the
-    // block; the first 8 partial outputs of every thread go out before the
-    // weights are known.
+    // Each wave owns qw of the head's nq output quads and does its whole
+    // merge alone, with no barrier: lane (part, quad) sums the splits
+    // part, part + pw, ... of its quad in that order, then the pw parts meet
+    // in a fixed xor tree of shuffles. Every wave computes the weights
+    // itself from all the (max, sum) pairs (at most 256, 4 per lane). The
+    // first 8 partial outputs of every lane go out with those loads.
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nq = hd / 4;
-    const uint32_t P = 256 / nq;
-    const uint32_t q = tid % nq;
-    const uint32_t part = tid / nq;
-    const auto o_off = [&](uint32_t j) { return part < P && j < S ? j * o_stride + 16 * q : buffer_oob; };
+    const uint32_t qw = (nq + 3) / 4;
+    const uint32_t qwp = qw <= 1 ? 1 : qw <= 2 ? 2 : qw <= 4 ? 4 : qw <= 8 ? 8 : 16;  // a power of two
+    const uint32_t pw = 64 / qwp;
+    const uint32_t ql = ln % qwp;
+    const uint32_t part = ln / qwp;
+    const uint32_t quad = w * qw + ql;
+    const bool mine = ql < qw && quad < nq;
+    const auto o_off = [&](uint32_t j) { return mine && j < S ? j * o_stride + 16 * quad : buffer_oob; };
     f4 ov[8];
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
-        ov[i] = __builtin_bit_cast(f4, buffer_load16(o_r, o_off(part + i * P)));
+        ov[i] = __builtin_bit_cast(f4, buffer_load16(o_r, o_off(part + i * pw)));
     }
-
-    // Phase 1 (wave 0): lane l holds splits l, l + 64, ...
-    if (tid < 64) {
-        constexpr uint32_t per_lane = decode_max_splits / 64;
-        float mj[per_lane], lj[per_lane];
+    constexpr uint32_t per_lane = decode_max_splits / 64;
+    float mj[per_lane], lj[per_lane];
 #pragma unroll
-        for (uint32_t i = 0; i < per_lane; ++i) {
-            const uint32_t j = ln + 64 * i;
-            const uint32_t off = j < S ? j * ml_stride : buffer_oob;
-            mj[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_r, off, 0, 0));
-            lj[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_r, off == buffer_oob ? off : off + 4, 0, 0));
-        }
-        float mx = -INFINITY;
+    for (uint32_t i = 0; i < per_lane; ++i) {
+        const uint32_t j = ln + 64 * i;
+        const uint32_t off = j < S ? j * ml_stride : buffer_oob;
+        mj[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_r, off, 0, 0));
+        lj[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_r, off == buffer_oob ? off : off + 4, 0, 0));
+    }
+    float mx = -INFINITY;
 #pragma unroll
-        for (uint32_t i = 0; i < per_lane; ++i) {
-            mj[i] = ln + 64 * i < S ? mj[i] : -INFINITY;
-            mx = fmaxf(mx, mj[i]);
-        }
-        mx = wave_reduce_max(mx);
-        float sum = 0.0f;
+    for (uint32_t i = 0; i < per_lane; ++i) {
+        mj[i] = ln + 64 * i < S ? mj[i] : -INFINITY;
+        mx = fmaxf(mx, mj[i]);
+    }
+    mx = wave_reduce_max(mx);
+    float sum = 0.0f;
 #pragma unroll
-        for (uint32_t i = 0; i < per_lane; ++i) {
-            mj[i] = fast_exp2((mj[i] - mx) * c);  // 0 for absent splits
-            sum += lj[i] * mj[i];
-        }
-        sum = wave_reduce_sum(sum);
-        const float inv = 1.0f / sum;
+    for (uint32_t i = 0; i < per_lane; ++i) {
+        mj[i] = fast_exp2((mj[i] - mx) * c);  // 0 for absent splits
+        sum += lj[i] * mj[i];
+    }
+    sum = wave_reduce_sum(sum);
+    const float inv = 1.0f / sum;
 #pragma unroll
-        for (uint32_t i = 0; i < per_lane; ++i) {
-            const uint32_t j = ln + 64 * i;
-            if (j < S) {
-                wts[j] = mj[i] * inv;
+    for (uint32_t i = 0; i < per_lane; ++i) {
+        mj[i] *= inv;  // the weight of split ln + 64 i
+    }
+    // The weights of splits j0 + i pw + part, j0 a multiple of 8 pw: split j
+    // is lane j % 64 of slot j / 64 (uniform: pw divides 64). Every lane
+    // takes part in the shuffles, all 8 issued before any is used.
+    const auto weights = [&](uint32_t j0, float (&wt)[8]) {
+        if (S <= 64) {  // one slot
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                wt[i] = __shfl(mj[0], static_cast<int>((j0 + i * pw + part) % 64), 64);
             }
+            return;
         }
-    }
-    __syncthreads();
-    // Phase 2: out = sum_j w_j O_j, splits in a fixed order per thread.
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint32_t slot = (j0 + i * pw) / 64;
+            const float src = slot == 0 ? mj[0] : slot == 1 ? mj[1] : slot == 2 ? mj[2] : mj[3];
+            wt[i] = __shfl(src, static_cast<int>((j0 + i * pw + part) % 64), 64);
+        }
+    };
     f4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+    float wt[8];
+    weights(0, wt);
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t j = part + i * P;
-        if (part < P && j < S) {
-            acc += wts[j] * ov[i];
-        }
+        acc += wt[i] * ov[i];  // 0 * 0 past the splits
     }
-    for (uint32_t j = part + 8 * P; j < S; j += 8 * P) {
+    for (uint32_t j0 = 8 * pw; j0 < S; j0 += 8 * pw) {
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
-            ov[i] = __builtin_bit_cast(f4, buffer_load16(o_r, o_off(j + i * P)));
+            ov[i] = __builtin_bit_cast(f4, buffer_load16(o_r, o_off(j0 + i * pw + part)));
         }
+        weights(j0, wt);
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
-            if (part < P && j + i * P < S) {
-                acc += wts[j + i * P] * ov[i];
-            }
+            acc += wt[i] * ov[i];
         }
     }
-    if (part < P) {
-        acc_lds[part * nq + q] = acc;
-    }
-    __syncthreads();
-    if (static_cast<uint32_t>(tid) < nq) {
-        f4 sum = acc_lds[tid];
-        for (uint32_t p2 = 1; p2 < P; ++p2) {
-            sum += acc_lds[p2 * nq + tid];
+    for (uint32_t m = qwp; m < 64; m <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc[e] += __shfl_xor(acc[e], static_cast<int>(m), 64);
         }
-        *reinterpret_cast<f4*>(s.out + (static_cast<std::size_t>(g) * group + h) * hd + 4 * tid) = sum;
     }
+    if (part == 0 && mine) {
+        *reinterpret_cast<f4*>(s.out + (static_cast<std::size_t>(g) * group + h) * hd + 4 * quad) = acc;
+    }
+#ifdef SYN_DECODE_STAMPS
+    DECODE_STAMP(0);
+    if (tid == 0 && u < decode_stamp_merges) {
+        decode_stamp_merge[2 * u] = entry_;
+        decode_stamp_merge[2 * u + 1] = stamp_[0];
+    }
+#endif
 }
 
 template <int HDP, class A>
@@ -867,3 +941,22 @@ hipError_t launch_decode(const decode_rope_args& a, uint32_t q_dtype, hipStream_
 }
 
 }  // namespace syn
+
+#ifdef SYN_DECODE_STAMPS
+// The timing build's stamps of the last decode launches, copied to the host
+// (synchronous): split[decode_stamp_blocks][4 waves][decode_stamp_points],
+// merge[decode_stamp_merges][entry, end] and the previous launch's merge
+// stamps in the same layout. 0 = not written.
+extern "C" int syn_hip_decode_stamps(unsigned long long* split, unsigned long long* merge,
+                                     unsigned long long* prev_merge) {
+    hipError_t e = hipMemcpyFromSymbol(split, HIP_SYMBOL(syn::decode_stamp_split), sizeof(syn::decode_stamp_split));
+    if (e == hipSuccess) {
+        e = hipMemcpyFromSymbol(merge, HIP_SYMBOL(syn::decode_stamp_merge), sizeof(syn::decode_stamp_merge));
+    }
+    if (e == hipSuccess) {
+        e = hipMemcpyFromSymbol(prev_merge, HIP_SYMBOL(syn::decode_stamp_prev), sizeof(syn::decode_stamp_prev));
+    }
+    return static_cast<int>(e);
+}
+#endif
+

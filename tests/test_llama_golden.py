@@ -35,6 +35,9 @@ MODELS = ["llama_tiny_f32", "qwen2_tiny_f32", "mistral3_tiny_f32"]
 # and the same argmax (tests/sdk/llama_golden.cpp:58-73).
 QMODELS = {"llama_tiny": 2e-2, "qwen2_tiny": 2e-2, "mistral3_tiny": 5e-2}
 BOUND = 1e-4
+# Whole-model decode past 128 cached rows (online softmax): see
+# test_gpu_long_decode_against_the_cpu_restatement.
+LONG_BOUND = 2e-3
 
 
 def _load(name):
@@ -147,3 +150,35 @@ def test_gpu_quantized_decode_matches_llama_cpp(name):
     assert rel_rms(got[:1], host[:1])[0] < 1e-5
     assert max(rel_rms(got, host)) < QMODELS[name]
 
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", MODELS)
+def test_gpu_long_decode_against_the_cpu_restatement(name):
+    """Past 128 cached rows the decode step's softmax is online: it rounds
+    the unnormalised p to binary16 (a relative step of 2^-11 per attention
+    weight) where attend_group rounds the normalised one, so the reference's
+    1e-4 logit bound no longer holds by construction. This pins what it
+    becomes: 300 positions (the golden tokens repeated) on the device against
+    the CPU restatement of the same graph (oracle attention), max |d| /
+    max |ref| below LONG_BOUND at every position, and the same argmax
+    wherever the restatement's top two logits are further apart than twice
+    that error."""
+    from synapse_amd.llama import DeviceLlama
+    model, tokens, _ = _load(name)
+    seq = (tokens * 19)[:300]
+    want = decode_logits(model, seq, max_ctx=len(seq))
+    m = DeviceLlama(model, max_ctx=len(seq))
+    try:
+        got = np.stack([m.step(t, i) for i, t in enumerate(seq)])
+    finally:
+        m.close()
+    res = compare(got, want)
+    worst = max(e for e, _ in res)
+    print(f"{name}: worst rel max err over {len(seq)} positions {worst:.3g} "
+          f"(first 128: {max(e for e, _ in res[:128]):.3g})")
+    for i, ((err, same), r) in enumerate(zip(res, want)):
+        assert err < LONG_BOUND, f"{name} position {i}: rel max err {err:.3g}"
+        top = np.sort(r.astype(np.float64))[-2:]
+        if top[1] - top[0] > 2 * err * np.max(np.abs(r)):
+            assert same, f"{name} position {i}: argmax differs with a clear margin"

@@ -43,7 +43,7 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
 # HBM bytes one config-2 decode step moves (split + merge kernels), from two
 # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a copy of known
 # size; profiles/decode_c2_pmc_traffic.md has the runs and the factors.
-DECODE_TRAFFIC_BYTES = 18_254_080
+DECODE_TRAFFIC_BYTES = 18_196_480
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 matrix, TFLOP/s
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 matrix, TOP/s
 
@@ -241,7 +241,7 @@ def bench_decode_rope(hip: Hip, cfg: wl.Decode, steps: int, layers: int):
     return result
 
 
-def bench_prefill(hip: Hip, cfg: wl.Prefill, reps: int):
+def bench_prefill(hip: Hip, cfg: wl.Prefill, reps: int, graph: bool = True):
     """Config 3: the flash kernel alone (cache already appended) and the
     whole op (append + attend)."""
     qsz = cfg.n_heads * cfg.head_dim
@@ -271,21 +271,28 @@ def bench_prefill(hip: Hip, cfg: wl.Prefill, reps: int):
         check(L.syn_hip_attention(arena.handle, ctypes.byref(d)))
     hip.record(t1, stream)
     op_ms = hip.ms(t0, t1) / reps
-    # The append alone is shorter than a host call: replayed from a graph.
+    # The append alone is shorter than a host call: replayed from a graph
+    # (called one by one in profiling runs, where the host paces it).
     def appends():
         for i in range(reps):
             check(L.syn_hip_kv_append(arena.handle, ctypes.byref(cache), d.k_offset, d.v_offset, cfg.n, 0, SYN_F16))
 
     arena.sync()
-    with capi.HipGraph(arena, appends) as hg:
-        hg.upload()
-        hg.launch()
-        t0, t1 = hip.events(2)
+    t0, t1 = hip.events(2)
+    if graph:
+        with capi.HipGraph(arena, appends) as hg:
+            hg.upload()
+            hg.launch()
+            hip.record(t0, stream)
+            hg.launch()
+            hip.record(t1, stream)
+            append_ms = hip.ms(t0, t1) / reps
+            arena.sync()
+    else:
         hip.record(t0, stream)
-        hg.launch()
+        appends()
         hip.record(t1, stream)
         append_ms = hip.ms(t0, t1) / reps
-        arena.sync()
     arena.close()
     return kern_ms, op_ms, append_ms
 
@@ -601,7 +608,7 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=40, help="distinct KV states rotated over (>= 32)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-graph", action="store_true", help="skip the graph-replayed decode figure (profiling runs)")
+    ap.add_argument("--no-graph", action="store_true", help="no HIP graphs (profiling runs): decode steps and the append timing called one by one")
     ap.add_argument("--decode-only", action="store_true", help="same as --only decode")
     ap.add_argument("--only", choices=["decode", "prefill", "ragged", "vision", "gemv", "gemm"], default=None,
                     help="run one configuration (no JSON line unless it is decode)")
@@ -623,7 +630,7 @@ def main() -> int:
     if only in (None, "prefill"):
         p = wl.C3
         log(f"prefill {p.name}")
-        kms, op_ms, app_ms = bench_prefill(hip, p, 50)
+        kms, op_ms, app_ms = bench_prefill(hip, p, 50, graph=not args.no_graph)
         tf = p.flops() / (kms * 1e-3) / 1e12
         app_bytes = 2 * p.n * p.n_kv * p.head_dim * (2 + 2)  # K and V: binary16 rows in, cache rows out
         extra["prefill"] = {"kernel_us": round(kms * 1e3, 2), "tflops": round(tf, 1),

@@ -39,9 +39,13 @@ __device__ __forceinline__ void store16(void* p, u4 v) {
     *reinterpret_cast<u4*>(p) = v;
 }
 
-// Byte address of an LDS location (what M0 and ds_* addresses take).
+// Byte address of an LDS location (what M0 and ds_* addresses take): the low
+// 32 bits of its generic address (the shared aperture sits above 4 GiB and
+// starts on a 4 GiB boundary). Unlike an address-space cast this has no null
+// check, so a kernel keeps each LDS address in one scalar register instead
+// of a 64-bit pointer plus a compare and select per use.
 __device__ __forceinline__ uint32_t lds_address(const void* lds) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)lds));
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
 }
 
 // Raw buffer access: a 128-bit resource (base, byte limit) in scalar

@@ -47,10 +47,28 @@ __device__ __forceinline__ void pf_barrier() {
     lds_barrier();
 }
 
-// One 1 KB tile copy: lane l's 16 bytes at byte `offset` of r land at
-// lds + 16 l (offsets at or past r's limit land as zeros).
-__device__ __forceinline__ void pf_copy(rsrc r, char* lds, uint32_t offset) {
-    buffer_load16_lds(r, lds, offset);
+// One 1 KB tile copy: lane l's 16 bytes at byte `offset` of r land at LDS
+// byte address at + 16 l (offsets at or past r's limit land as zeros).
+__device__ __forceinline__ void pf_copy(rsrc r, uint32_t at, uint32_t offset) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(offset), "s"(r), "{m0}"(at) : "memory");
+}
+
+// v, which the compiler must treat as unknown here: keeps a value computed
+// from it next to its use instead of hoisted and held across a loop.
+__device__ __forceinline__ uint32_t pf_opaque(uint32_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+// The LDS byte address of a wave's first copy into a stage, in one scalar
+// register that the compiler must treat as new on every item: it then adds
+// each copy's constant offset as it sets M0, instead of keeping every copy's
+// address live in a register of its own across the loop (register pressure
+// that spilled scalar registers).
+__device__ __forceinline__ uint32_t pf_copy_base(const char* lds, uint32_t first) {
+    uint32_t at = lds_address(lds) + 1024 * first;
+    asm volatile("" : "+s"(at));
+    return at;
 }
 
 template <bool F16>
@@ -202,17 +220,19 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
         const rsrc k_res = make_rsrc(k_head + static_cast<std::size_t>(t0) * a.row, k_bytes - t0 * a.row * 2);
         const rsrc v_res = make_rsrc(v_head + t0, v_bytes - t0 * 2);
         const bool last = t0 + pf_bk > kv_end;
+        const uint32_t kb = pf_copy_base(sk, w);
+        const uint32_t vb = pf_copy_base(sv - 1024 * TK, w);
 #pragma unroll
         for (int i = 0; i < CPW; ++i) {
             const uint32_t j = w + 4 * i;
             if (j < TK) {
-                pf_copy(k_res, sk + 1024 * j, coff[i]);
+                pf_copy(k_res, kb + 4096 * i, coff[i]);
             } else if (j < TT) {
                 uint32_t off = coff[i];
                 if (last && 8 * ((64 * (j - TK) + ln) % VROWC) >= kv_end - t0) {
                     off = buffer_oob;
                 }
-                pf_copy(v_res, sv + 1024 * (j - TK), off);
+                pf_copy(v_res, vb + 4096 * i, off);
             }
         }
     };
@@ -470,10 +490,11 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
         my_pos = a.pos + my_q;
         kv_end = kv_end_of(qt);
         wave_last_pos = a.pos + min(a.n - 1, q_row0 + 31);
+        const uint32_t hd_here = pf_opaque(hd);  // (as in store)
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             const uint32_t d0 = H * HSPAN + 8 * st;
-            qv[st] = my_q < a.n && d0 < hd
+            qv[st] = my_q < a.n && d0 < hd_here
                          ? pf_load_q<QF16>(a.q, static_cast<std::size_t>(my_q) * a.q_row + h * hd + d0)
                          : as_h8(zero_u4());
         }
@@ -517,13 +538,15 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
         const rsrc k_res = make_rsrc(k_head + static_cast<std::size_t>(t0) * a.row, (ke - t0) * a.row * 2 - g * hd * 2);
         const rsrc v_res = make_rsrc(v_head + t0, v_bytes - t0 * 2);
         const bool last = t0 + pf_bk > ke;
+        const uint32_t kb = pf_copy_base(sk, wg);
+        const uint32_t vb = pf_copy_base(sv - 1024 * TK, wg);
 #pragma unroll
         for (int i = 0; i < CPW; ++i) {
             const uint32_t jj = wg + 4 * i;
             if (jj < TK) {
-                pf_copy(k_res, sk + 1024 * jj, coff[i]);
+                pf_copy(k_res, kb + 4096 * i, coff[i]);
             } else if (jj < TT) {
-                pf_copy(v_res, sv + 1024 * (jj - TK), last && 8 * vc[i] >= ke - t0 ? buffer_oob : coff[i]);
+                pf_copy(v_res, vb + 4096 * i, last && 8 * vc[i] >= ke - t0 ? buffer_oob : coff[i]);
             }
         }
     };
@@ -568,12 +591,16 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
         }
         const float inv = 1.0f / l_run;
         float* out = a.out + static_cast<std::size_t>(my_q) * a.q_row + h * hd;
+        // The dims' bounds compared here, where they are used: hoisted out of
+        // the item loop, their lane masks took 32 scalar registers for the
+        // whole kernel and spilled.
+        const uint32_t hd_here = pf_opaque(hd);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 const uint32_t d = 32 * n + 8 * b + 4 * H;
-                if (d < hd) {
+                if (d < hd_here) {
                     *reinterpret_cast<f4*>(out + d) =
                         f4{o[n][4 * b] * inv, o[n][4 * b + 1] * inv, o[n][4 * b + 2] * inv, o[n][4 * b + 3] * inv};
                 }

@@ -35,9 +35,12 @@ MODELS = ["llama_tiny_f32", "qwen2_tiny_f32", "mistral3_tiny_f32"]
 # and the same argmax (tests/sdk/llama_golden.cpp:58-73).
 QMODELS = {"llama_tiny": 2e-2, "qwen2_tiny": 2e-2, "mistral3_tiny": 5e-2}
 BOUND = 1e-4
-# Whole-model decode past 128 cached rows (online softmax): see
+# Whole-model decode past 128 cached rows (online softmax), against the CPU
+# restatement: measured worst 1.5e-4 (Llama), 1.1e-4 (Qwen2), 6.6e-4
+# (Mistral 3, whose YaRN RoPE also differs from the restatement by an ulp:
+# 2.5e-4 within the first 128 rows already). See
 # test_gpu_long_decode_against_the_cpu_restatement.
-LONG_BOUND = 2e-3
+LONG_BOUND = 1e-3
 
 
 def _load(name):

@@ -58,7 +58,7 @@ namespace syn {
 // first copies the previous launch's merge stamps aside, so one read after a
 // run of steps shows a whole step: previous merge, split, merge.
 constexpr uint32_t decode_stamp_blocks = 512;
-constexpr uint32_t decode_stamp_points = 9;
+constexpr uint32_t decode_stamp_points = 10;
 constexpr uint32_t decode_stamp_merges = 64;
 __device__ unsigned long long decode_stamp_split[decode_stamp_blocks * 4 * decode_stamp_points];
 __device__ unsigned long long decode_stamp_merge[decode_stamp_merges * 2];
@@ -201,6 +201,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // round trip to the kernel arguments (about half a microsecond) before
     // any wave's first K, V load.
     asm volatile("" : : "s"(s.len), "s"(s.n_splits), "s"(s.ctx_stride), "s"(p.scale_log2e));
+    DECODE_STAMP(9);
     const uint32_t cached = s.len - (s.k_new != nullptr ? 1u : 0u);
     const uint32_t t_begin = split * p.chunk;
     const uint32_t t_end = min(cached, t_begin + p.chunk);

@@ -24,8 +24,11 @@ import numpy as np
 from synapse_amd import capi
 from synapse_amd import workloads as wl
 
-POINTS = ["entry", "K, V loads issued", "q ready (LDS barrier)", "K landed, scores done", "softmax done",
-          "V landed, P.V done", "partials in LDS", "after the LDS barrier", "stores issued (end)"]
+# (stamp index, phase) in the order a wave passes them.
+POINTS = [(0, "entry"), (9, "kernel arguments in registers"), (1, "K, V loads issued"),
+          (2, "q ready (LDS barrier)"), (3, "K landed, scores done"), (4, "softmax done"),
+          (5, "V landed, P.V done"), (6, "partials in LDS"), (7, "after the LDS barrier"),
+          (8, "stores issued (end)")]
 BLOCKS, WAVES, MERGES = 512, 4, 64
 
 
@@ -95,7 +98,7 @@ def main(argv: list[str] | None = None) -> int:
 
     row_of("previous step: merge block entry", prev[:, 0])
     row_of("previous step: merge block end", prev[:, 1])
-    for k, name in enumerate(POINTS):
+    for k, name in POINTS:
         row_of(f"split wave: {name}", split[used][:, :, k].reshape(-1))
     row_of("merge block entry", merge[:, 0])
     row_of("merge block end", merge[:, 1])

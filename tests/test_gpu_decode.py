@@ -85,6 +85,16 @@ def test_decode_long_contexts(arena, ctx):
     assert_close(got, want, what=f"ctx {ctx}")
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hd,ctx", [(16, 1, 128, 32000), (8, 1, 40, 20000), (4, 1, 256, 16500)])
+def test_decode_merge_of_up_to_256_splits(arena, n_heads, n_kv, hd, ctx):
+    """One KV head keeps the chunk at 128 positions up to 256 splits: the
+    merge kernel's weights then come from all four of a lane's split slots
+    (250, 157 and 129 splits here), for head sizes whose output quads fill
+    the waves unevenly (hd 40: 10 quads over 4 waves)."""
+    got, want, _, _ = _case(arena, n_heads, n_kv, hd, ctx, seed=ctx + hd, theta=500000.0)
+    assert_close(got, want, what=f"ctx {ctx}, hd {hd}")
+
+
 @pytest.mark.parametrize("n_heads,n_kv,hd", [(8, 8, 32), (4, 2, 16), (16, 8, 64), (28, 4, 128), (32, 2, 128),
                                              (16, 1, 128), (8, 2, 80), (12, 4, 96), (8, 4, 256), (6, 3, 40)])
 def test_decode_head_layouts(arena, n_heads, n_kv, hd):

@@ -58,7 +58,7 @@ namespace syn {
 // first copies the previous launch's merge stamps aside, so one read after a
 // run of steps shows a whole step: previous merge, split, merge.
 constexpr uint32_t decode_stamp_blocks = 512;
-constexpr uint32_t decode_stamp_points = 10;
+constexpr uint32_t decode_stamp_points = 12;
 constexpr uint32_t decode_stamp_merges = 64;
 __device__ unsigned long long decode_stamp_split[decode_stamp_blocks * 4 * decode_stamp_points];
 __device__ unsigned long long decode_stamp_merge[decode_stamp_merges * 2];
@@ -310,8 +310,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     // rounded to binary16 as attend_group rounds q (S/kernels/attention.hpp:204-206).
     h8 qv[NS];
     // A fused RoPE step rotates the q rows and the new K row in LDS, once per
-    // block, after they have landed: wave 0 first builds every pair's cos
-    // and sin into a table, then the pairs of every row are rotated in place
+    // block, after they have landed: wave 0 has built every pair's cos and
+    // sin into a table (here, when frequency factors had to land first),
+    // then the pairs of every row are rotated in place
     // (q also times the temperature factor), and the staging below reads the
     // rotated f32 rows as it reads unrotated ones.
     float* rope_tab = reinterpret_cast<float*>(lds_bytes + rope_lds_offset(group, hd));
@@ -319,10 +320,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
     float* rope_th = reinterpret_cast<float*>(ff_lds + 1024);  // the pairs' angles
     const auto rope_rows = [&]() {
         const uint32_t half = hd / 2;
-        if (w == 0) {
-            const float* ff = a_rope(a).freq_factors != nullptr ? reinterpret_cast<const float*>(ff_lds) : nullptr;
-            rope_table(a_rope(a), rope_th, half, ff, rope_tab, static_cast<uint32_t>(ln));
+        if (w == 0 && a_rope(a).freq_factors != nullptr) {  // (without factors: built before the loads)
+            rope_table(a_rope(a), rope_th, half, reinterpret_cast<const float*>(ff_lds), rope_tab,
+                       static_cast<uint32_t>(ln));
         }
+        DECODE_STAMP(10);
         lds_barrier();
         const bool normal = a_rope(a).mode == 0;
         const float q_scale = a_rope(a).temp_floor_len != 0
@@ -341,6 +343,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
             x[i0] = rope_first(x0, x1, cs, sn) * f;
             x[i1] = rope_second(x0, x1, cs, sn) * f;
         }
+        DECODE_STAMP(11);
     };
     const auto convert_q = [&](bool kv_issued) {
         // Wait for this wave's copies (q, the new row) only: the K, V loads
@@ -476,22 +479,33 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
             load16_lds(reinterpret_cast<const char*>(a.r.freq_factors) + off, ff_lds);
         }
     }
+    if constexpr (ROPE) {
+        // The angles need neither q nor the factors, and without factors
+        // neither does the cos / sin table: wave 0 builds them before its
+        // K, V loads go out. (After the loads, the chain and the table took
+        // wave 0 ~1.2 us past the moment q had landed, on every block's
+        // critical path: a wave's loads take ~1.5 us to issue, and the
+        // other waves waited at the barrier for the table.) With factors
+        // the table waits for their copy, with q.
+        if (w == 0) {
+            if (ln == 0) {
+                rope_angles(new_t, a.r.theta_scale, hd / 2, rope_th);
+            }
+            if (a.r.freq_factors == nullptr) {
+                rope_table(a.r, rope_th, hd / 2, static_cast<const float*>(nullptr), rope_tab,
+                           static_cast<uint32_t>(ln));
+            }
+        }
+    }
     // A fused RoPE step loads unconditionally: a wave with no positions
     // reads past the resources' limits and gets zeros without memory
     // traffic. (Guarded, the results met zero-initialised registers at the
     // join, the compiler moved each as soon as it landed, waiting for it
-    // between the loads, and the angle chain below ran only after that.)
+    // between the loads.)
     if (ROPE || tb < t_end) {
         load_kv(tb, kr, vr);
     }
     DECODE_STAMP(1);
-    if constexpr (ROPE) {
-        // The angles need neither q nor the factors: lane 0 of wave 0 runs
-        // their chain while the loads are in flight.
-        if (w == 0 && ln == 0) {
-            rope_angles(new_t, a.r.theta_scale, hd / 2, rope_th);
-        }
-    }
     convert_q(ROPE || tb < t_end);
     DECODE_STAMP(2);
     float* lds_ml = reinterpret_cast<float*>(lds_bytes + q_lds_bytes(group, hd) + new_lds_bytes(hd));

@@ -1,14 +1,16 @@
 """Phase timeline of one config-2 decode step, from the timing build's stamps.
 
     python -m synapse_amd.build --stamps
-    python -m synapse_amd.decode_phases [--steps K] [--out FILE]
+    python -m synapse_amd.decode_phases [--steps K] [--rope] [--out FILE]
 
 Runs config 2 (Llama-3-8B heads, 4096 cached rows + the step's row) as the
 bench does: K steps over 40 rotating KV states, replayed from one HIP graph,
 on libsynapse_hip_stamps.so, whose decode kernels record s_memrealtime stamps
 (100 MHz). The stamps of the graph's last step are then read: every wave of
 the split kernel at its phase points, every merge block's entry and end, and
-the previous step's merge blocks. Prints a markdown table of each phase's
+the previous step's merge blocks. With --rope each step is the fused
+RoPE step (syn_hip_attention_rope: q and the step's K row rotated in the
+split kernel, Llama 3's RoPE at theta 500000). Prints a markdown table of each phase's
 spread over the waves, in microseconds after the step's first split-kernel
 wave entered. The stamps perturb the kernels slightly (each is a scalar
 memory read of the clock): the step is about 0.2 us longer than in the
@@ -26,7 +28,7 @@ from synapse_amd import workloads as wl
 
 # (stamp index, phase) in the order a wave passes them.
 POINTS = [(0, "entry"), (9, "kernel arguments in registers"), (1, "K, V loads issued"),
-          (2, "q ready (LDS barrier)"), (3, "K landed, scores done"), (4, "softmax done"),
+          (10, "RoPE: cos/sin table built"), (11, "RoPE: q and the new row rotated"), (2, "q ready (LDS barrier)"), (3, "K landed, scores done"), (4, "softmax done"),
           (5, "V landed, P.V done"), (6, "partials in LDS"), (7, "after the LDS barrier"),
           (8, "stores issued (end)")]
 BLOCKS, WAVES, MERGES = 512, 4, 64
@@ -35,6 +37,7 @@ BLOCKS, WAVES, MERGES = 512, 4, 64
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--rope", action="store_true", help="time the fused RoPE step (syn_hip_attention_rope)")
     ap.add_argument("--out", default=None, help="also write the table to this file")
     args = ap.parse_args(argv)
     stamps_lib = capi.ROOT / "libsynapse_hip_stamps.so"
@@ -52,7 +55,7 @@ def main(argv: list[str] | None = None) -> int:
     scratch_bytes = int(L.syn_hip_attention_scratch_bytes(cfg.n_heads, cfg.n_kv, cfg.head_dim, max_ctx, 1))
     per_layer = capi.kv_state_bytes(max_ctx, cfg.n_kv, cfg.head_dim) + 2 * capi.align(qsz * 4) + \
         2 * capi.align(row * 4) + 4096
-    arena = capi.Arena(layers * per_layer + scratch_bytes + (1 << 20))
+    arena = capi.Arena(layers * (per_layer + 2 * capi.align(qsz * 4)) + scratch_bytes + (1 << 20))
     kc, vc, q, k, v = wl.decode_inputs(cfg)
     scratch = arena.alloc(scratch_bytes)
     descs = []
@@ -65,8 +68,20 @@ def main(argv: list[str] | None = None) -> int:
                                    scale=cfg.scale, q_dtype=capi.SYN_F32, kv_dtype=capi.SYN_F32))
     arena.sync()
     refs = [ctypes.byref(d) for d in descs]
-    with capi.HipGraph(arena, lambda: [capi.check(L.syn_hip_attention(arena.handle, refs[i % layers]))
-                                       for i in range(args.steps)]) as g:
+    theta_scale = float(np.float32(cfg.theta) ** np.float32(-2.0 / cfg.head_dim))
+    ropes = [capi.AttnRopeDesc(q_out_offset=arena.alloc(qsz * 4), k_out_offset=arena.alloc(qsz * 4),
+                               freq_factors_offset=capi.NO_OFFSET, theta_scale=theta_scale, mode=0,
+                               freq_scale=1.0, ext_factor=0.0, attn_factor=1.0, corr_low=0.0, corr_high=0.0,
+                               temp_scale=0.0, temp_floor_len=0) for _ in range(layers)]
+    rrefs = [ctypes.byref(r) for r in ropes]
+
+    def step(i):
+        if args.rope:
+            capi.check(L.syn_hip_attention_rope(arena.handle, refs[i % layers], rrefs[i % layers]))
+        else:
+            capi.check(L.syn_hip_attention(arena.handle, refs[i % layers]))
+
+    with capi.HipGraph(arena, lambda: [step(i) for i in range(args.steps)]) as g:
         g.upload()
         g.launch()
         arena.sync()
@@ -84,7 +99,8 @@ def main(argv: list[str] | None = None) -> int:
     used = split[:, 0, 0] > 0
     t0 = split[used][:, :, 0].min()
     us = lambda x: (x - t0) * 0.01  # noqa: E731  (100 MHz clock)
-    lines = [f"config 2 decode step (the last of {args.steps} graph-replayed steps over {layers} KV states): "
+    lines = [f"config 2 decode step{' with fused RoPE' if args.rope else ''} (the last of {args.steps} graph-replayed "
+             f"steps over {layers} KV states): "
              f"{int(used.sum())} split blocks x {WAVES} waves, {int((merge[:, 0] > 0).sum())} merge blocks; "
              "us after the first split wave's entry", "",
              "| phase | min | p10 | p50 | p90 | max |", "|---|---|---|---|---|---|"]

@@ -71,6 +71,16 @@ __device__ __forceinline__ uint32_t pf_copy_base(const char* lds, uint32_t first
     return at;
 }
 
+// Block j of a row of n_heads blocks -> its query head. Consecutive blocks
+// go to the 8 XCDs in turn, so with n_heads a multiple of 8 block j takes
+// head (j % 8) * (n_heads / 8) + j / 8: XCD x holds heads x * n_heads / 8
+// onwards, and since the query heads of one KV head are consecutive, each
+// XCD's L2 holds the K and V of whole KV heads (for Llama-3-8B's 32 heads
+// over 8 KV heads, one KV head per XCD) instead of parts of four.
+__device__ __forceinline__ uint32_t pf_head(uint32_t j, uint32_t n_heads) {
+    return n_heads % 8 == 0 ? (j % 8) * (n_heads / 8) + j / 8 : j;
+}
+
 template <bool F16>
 __device__ __forceinline__ h8 pf_load_q(const void* base, std::size_t index) {
     if constexpr (F16) {
@@ -157,7 +167,7 @@ __global__ __launch_bounds__(256, HD <= 128 ? 2 : 1) void prefill_kernel(const f
     // on a CU carry about equal causal work.
     const uint32_t n_qt = (a.n + pf_bq - 1) / pf_bq;
     const uint32_t rank = blockIdx.x / a.n_heads;
-    const uint32_t h = blockIdx.x % a.n_heads;
+    const uint32_t h = pf_head(blockIdx.x % a.n_heads, a.n_heads);
     const uint32_t heavy = (n_qt + 1) / 2;
     const uint32_t qt = rank < heavy ? n_qt - 1 - rank : rank - heavy;
     const uint32_t g = h / a.group;
@@ -462,7 +472,7 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
     const uint32_t hd = a.hd;
     const uint32_t n_qt = (a.n + pf_bq - 1) / pf_bq;
     const uint32_t pr = blockIdx.x / a.n_heads;
-    const uint32_t h = blockIdx.x % a.n_heads;
+    const uint32_t h = pf_head(blockIdx.x % a.n_heads, a.n_heads);
     const uint32_t tA = pr, tB = n_qt - 1 - pr;  // tA == tB: the middle tile of an odd count
     const uint32_t g = h / a.group;
     const float c = a.scale_log2e;

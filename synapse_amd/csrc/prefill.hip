@@ -649,13 +649,16 @@ __global__ __launch_bounds__(512, 2) void prefill_pair_kernel(const flash_args a
             __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
         }
         if (t0 + pf_bk - 1 > a.pos + q_row0 || t0 + pf_bk > kv_end) {
-            const uint32_t lim = max(min(my_pos + 1, kv_end), t0) - t0;
+            // Key 32 e + 16 (i / 8) + 8 H + i % 8 of the tile is kept when it
+            // is below the bound; the lane's half moved to the bound, each
+            // compare is against a constant and no key index is held in a
+            // register (that took 20 VGPRs for the whole kernel).
+            const int lim = static_cast<int>(max(min(my_pos + 1, kv_end), t0) - t0) - 8 * H;
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const uint32_t kk = 32 * e + 16 * (i >> 3) + 8 * H + (i & 7);
-                    sc[e][i] = kk < lim ? sc[e][i] : -INFINITY;
+                    sc[e][i] = 32 * e + 16 * (i >> 3) + (i & 7) < lim ? sc[e][i] : -INFINITY;
                 }
             }
         }

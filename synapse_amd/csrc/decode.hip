@@ -31,11 +31,12 @@
 // write-through or read with agent-scope loads (plain loads on another CU
 // never see them), and the handoff -- store acknowledged, arrival counter,
 // poll, partial loads -- costs three or four loaded memory round trips,
-// more than the second launch. The merge stages through LDS: one wave turns
-// the splits' (max, sum) into weights (its wave-wide max and sum by DPP and
-// permlane swaps), then all threads stream the partial outputs with
-// independent 16-byte loads. Each output sums its
-// splits in a fixed order, so results are deterministic.
+// more than the second launch. The merge needs no LDS and no barrier: each
+// wave of a merge block owns a quarter of the head's output and turns all
+// the splits' (max, sum) into weights itself (wave-wide max and sum by DPP
+// and permlane swaps), then streams the partial outputs with independent
+// 16-byte loads. Each output sums its splits in a fixed order, so results
+// are deterministic.
 //
 // A single-token step passes its new K, V row (k_new, v_new). The waves'
 // steps cover the cached rows only; the block of the last split also rounds

@@ -274,8 +274,18 @@ __host__ __device__ constexpr uint32_t resident_max_keys(uint32_t hdp) {
     return np;
 }
 
+// Staggered staging. Two blocks share each CU, and a block computes nothing
+// until its whole unit has landed; when both stage at once, both land late.
+// Blocks from..to-1 -- the second block on their CU, with the grid dealt to
+// the CUs in order -- wait `ticks` of the 100 MHz constant clock first: the
+// time the first block's bytes take at peak HBM bandwidth shared over the
+// CUs. The first block then computes while the second's bytes land.
+struct resident_stagger {
+    uint32_t from, to, ticks;
+};
+
 template <int HD>
-__global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
+__global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a, const resident_stagger st) {
     constexpr int NS = HD / 16;      // k-steps of the score product
     constexpr int NT = HD / 32;      // 32-dim tiles of the output
     constexpr int KCPR = HD / 8;     // 16-byte chunks of a K row
@@ -679,6 +689,12 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
     };
 
     u4 kc[KC], vc[VC][2], qc[QT][NS], tq;
+    if (blockIdx.x >= st.from && blockIdx.x < st.to) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__builtin_amdgcn_s_memrealtime() - t0 < st.ticks) {
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
     load_unit(kc, vc, qc, tq);
     store_unit(kc, vc);
     lds_barrier();
@@ -693,7 +709,14 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a) {
 template <int HD>
 hipError_t launch_resident(const flash_args& a, hipStream_t stream) {
     const dim3 grid(a.n_heads * a.batch);
-    resident_kernel<HD><<<grid, 256, resident_unit_bytes(a.n, HD), stream>>>(a);
+    resident_stagger st{0, 0, 0};
+    const uint32_t cus = device_cu_count();
+    if (cus > 0 && grid.x > cus) {
+        // A unit's staged bytes: its K, V and q rows in binary16.
+        const double bytes = 3.0 * a.n * a.hd * 2;
+        st = {cus, std::min(grid.x, 2 * cus), static_cast<uint32_t>(bytes * cus / 8e12 * 1e8)};
+    }
+    resident_kernel<HD><<<grid, 256, resident_unit_bytes(a.n, HD), stream>>>(a, st);
     return hipGetLastError();
 }
 

@@ -417,7 +417,7 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a, co
     float m_run = -INFINITY, l_run = 0.0f;
     h8 qv[NS];
     // E 32-key slices from key t0 (keys past n masked).
-    const auto step = [&]<int E>(uint32_t t0) __attribute__((always_inline)) {
+    const auto step = [&]<int E, bool FIRST>(uint32_t t0) __attribute__((always_inline)) {
         f16v sc[E];
         // All K operands are read before the first product, and (up to head
         // dim 64, where the registers are there) the V^T operands right after
@@ -470,7 +470,11 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a, co
             }
         }
         h8 pv[2 * E];
-        online_softmax<E, NT>(sc, c, m_run, l_run, o, pv);
+        if constexpr (FIRST) {
+            first_softmax<E>(sc, c, m_run, l_run, pv);
+        } else {
+            online_softmax<E, NT>(sc, c, m_run, l_run, o, pv);
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             // V^T row 32t + qi, keys t0 + 8H + 16 s ..
@@ -534,12 +538,20 @@ __global__ __launch_bounds__(256, 2) void resident_kernel(const flash_args a, co
             }
             m_run = -INFINITY;
             l_run = 0.0f;
-            uint32_t t0 = 0;
+            // The first step apart (first_softmax), then the rest.
+            uint32_t t0;
+            if (np >= 64) {
+                step.template operator()<2, true>(0);
+                t0 = 64;
+            } else {
+                step.template operator()<1, true>(0);
+                t0 = np;
+            }
             for (; t0 + 64 <= np; t0 += 64) {
-                step.template operator()<2>(t0);
+                step.template operator()<2, false>(t0);
             }
             if (t0 < np) {
-                step.template operator()<1>(t0);
+                step.template operator()<1, false>(t0);
             }
             if (my_q < n) {
                 const float inv = 1.0f / l_run;

@@ -1,5 +1,5 @@
-// softmax.hpp — the online softmax step shared by the matrix-core attention
-// kernels (prefill.hip, flash.hip).
+// softmax.hpp — the online softmax step of the bidirectional matrix-core
+// attention kernel (flash.hip).
 //
 // Layout: a 32x32x16 score product S^T = K . Q^T leaves, for E 32-key slices,
 // 16 scores per lane: lane (H, qi) holds keys 16(i/8) + 8H + i%8 of each
@@ -47,26 +47,31 @@ __device__ __forceinline__ float softmax_probs(const f16v (&sc)[E], float c, flo
     return sum32(ps);
 }
 
+// A sweep's first step: no query of the wave has a max yet, so the max is
+// taken first (the optimistic pass would send every query to the rescale
+// path and compute its probabilities twice).
+template <int E>
+__device__ __forceinline__ void first_softmax(const f16v (&sc)[E], float c, float& m_run, float& l_run,
+                                              h8 (&pv)[2 * E]) {
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            tmax = fmaxf(tmax, sc[e][i]);
+        }
+    }
+    m_run = max32(tmax);
+    l_run += softmax_probs<E>(sc, c, m_run, pv);
+}
+
+// The later steps. The caller takes the first step with first_softmax, out
+// of its loop: with both forms in the loop body, the compiler kept the
+// output accumulators in two register ranges and copied them across on
+// every step (48 moves per step at hd 64).
 template <int E, int NT>
 __device__ __forceinline__ void online_softmax(const f16v (&sc)[E], float c, float& m_run, float& l_run,
                                                f16v (&o)[NT], h8 (&pv)[2 * E]) {
-    // No query of the wave has a max yet (a sweep's first step): take the
-    // max first. The optimistic pass would go to the rescale path for every
-    // query and compute the probabilities twice; this gives the same values
-    // (the sum and O are still 0, so the rescale would not change them).
-    if (__builtin_amdgcn_ballot_w64(m_run != -INFINITY) == 0) {
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                tmax = fmaxf(tmax, sc[e][i]);
-            }
-        }
-        m_run = max32(tmax);
-        l_run += softmax_probs<E>(sc, c, m_run, pv);
-        return;
-    }
     float psum = softmax_probs<E>(sc, c, m_run, pv);
     const bool grow = m_run == -INFINITY || !(psum <= 256.0f);
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -75,7 +80,11 @@ __device__ __forceinline__ void online_softmax(const f16v (&sc)[E], float c, flo
         for (int e = 0; e < E; ++e) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                tmax = fmaxf(tmax, sc[e][i]);
+                // Opaque to the optimiser: otherwise it hoists this max out of
+                // the rare branch and every step pays for it.
+                float x = sc[e][i];
+                asm volatile("" : "+v"(x));
+                tmax = fmaxf(tmax, x);
             }
         }
         tmax = max32(tmax);

@@ -155,7 +155,7 @@ __device__ __forceinline__ const rope_params& a_rope(const A& a) {
 // takes the whole-softmax path below; launches without one compile it out
 // (it costs the online path about 60 registers).
 template <int HDP, bool QF16, bool SHORT, class A>
-__global__ __launch_bounds__(256) void decode_kernel(const A a) {
+__global__ __launch_bounds__(256, SHORT && HDP <= 128 ? 2 : 1) void decode_kernel(const A a) {
     using T = decode_traits<A>;
     constexpr bool MULTI = T::multi;
     constexpr bool ROPE = std::is_same_v<A, decode_rope_args>;
@@ -432,16 +432,32 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
         }
     };
 
-    // One online-softmax step: p = exp(s - running max) rounded to f16, the
-    // running sum and O rescaled when the max grows.
+    // One online-softmax step: p = exp(s - running max) rounded to f16. The
+    // running max is lazy: a head's max is raised only when the step's rises
+    // more than 8 above it in the exp2 domain (its p then stay below 2^8,
+    // which binary16 holds), and only then are its sum and O rescaled --
+    // never on a wave's first step, whose O is still zero. O lives in the
+    // accumulation registers: rescaled on every step, all of it was read out
+    // and written back each time.
+    bool o_zero = true;
     const auto step = [&](uint32_t tb, u4 (&kr)[2][NS], u4 (&vr)[NT]) {
         const uint32_t tv = tb + 8 * G;
         f4 sc[2];
         const float bm = scores(tv, kr, sc);
         DECODE_STAMP(3);
-        const float m_new = fmaxf(m_run, bm);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = fast_exp2((m_run - m_use) * c);
+        const bool grow = (bm - m_run) * c > 8.0f;  // false for bm = -inf
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float alpha = grow ? fast_exp2((m_run - bm) * c) : 1.0f;  // 0 from m_run = -inf
+            m_run = grow ? bm : m_run;
+            l_run *= alpha;
+            if (!o_zero) {
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    o[n] *= alpha;
+                }
+            }
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         h8 pa;
         float ps = 0.0f;
 #pragma unroll
@@ -453,15 +469,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const A a) {
                 ps += static_cast<float>(ph);
             }
         }
-        l_run = l_run * alpha + sum32(sum16(ps));
-        m_run = m_new;
-        // The O^T accumulator's column is this lane's head: rescale by its own alpha.
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            o[n] *= alpha;
-        }
+        l_run += sum32(sum16(ps));
         DECODE_STAMP(4);
         accumulate(tv, vr, pa);
+        o_zero = false;
         DECODE_STAMP(5);
     };
 

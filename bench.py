@@ -178,11 +178,14 @@ def bench_decode(hip: Hip, cfg: wl.Decode, steps: int, warmup: int, layers: int,
     return step_ms, det
 
 
-def bench_decode_rope(hip: Hip, cfg: wl.Decode, steps: int, layers: int):
+def bench_decode_rope(hip: Hip, cfg: wl.Decode, steps: int, layers: int, graph: bool = True):
     """Config 2 with Llama 3's RoPE applied to the step's q and k: the layer's
     op_rope(q), op_rope(k) and op_attention as one syn_hip_attention_rope
     call (the split kernel rotates in LDS; 2 launches) against the three
-    separate calls (4 launches). Same rotating KV states as bench_decode."""
+    separate calls (4 launches). Same rotating KV states as bench_decode, and
+    timed the same way: with graph, `steps` steps captured into one HIP graph
+    whose launch is the timed region (a warm-up graph of the same steps runs
+    right ahead of it); without, called one by one."""
     row = cfg.n_kv * cfg.head_dim
     max_ctx = cfg.ctx + 1
     qsz = cfg.n_heads * cfg.head_dim
@@ -229,15 +232,27 @@ def bench_decode_rope(hip: Hip, cfg: wl.Decode, steps: int, layers: int):
             fn(i)
         arena.sync()
         t0, t1 = hip.events(2)
-        hip.record(t0, stream)
-        for i in range(steps):
-            fn(i)
-        hip.record(t1, stream)
+        if graph:
+            with capi.HipGraph(arena, lambda: [fn(i) for i in range(steps)]) as hg:
+                hg.upload()
+                hg.launch()
+                arena.sync()
+                hg.launch()
+                hip.record(t0, stream)
+                hg.launch()
+                hip.record(t1, stream)
+                arena.sync()
+        else:
+            hip.record(t0, stream)
+            for i in range(steps):
+                fn(i)
+            hip.record(t1, stream)
         result[name] = round(hip.ms(t0, t1) / steps * 1e3, 3)
     out = arena.download(separate[0][3].out_offset, (qsz,), np.float32)
     assert np.all(np.isfinite(out))
     arena.close()
-    result.update({"launches_fused": 2, "launches_separate": 4, "steps": steps})
+    result.update({"launches_fused": 2, "launches_separate": 4, "steps": steps,
+                   "timing": "HIP-graph launch of the timed steps" if graph else "steps called one by one"})
     return result
 
 
@@ -676,7 +691,7 @@ def main() -> int:
     value = nbytes / (step_ms * 1e-3) / 1e9
     log(f"decode: {step_ms * 1e3:.2f} us/step -> {value:.0f} GB/s ({det['timing']}); called one by one: "
         f"{det['eager_ms_per_step'] * 1e3:.2f} us/step, wall {det['wall_ms_per_step'] * 1e3:.2f} us/step")
-    extra["decode_rope"] = bench_decode_rope(hip, cfg, 400, args.layers)
+    extra["decode_rope"] = bench_decode_rope(hip, cfg, 400, args.layers, graph=not args.no_graph)
     log(f"decode with RoPE: {extra['decode_rope']}")
     extra.update({"decode_step_us": round(step_ms * 1e3, 3),
                   "decode_timing": det["timing"],

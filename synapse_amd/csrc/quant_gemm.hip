@@ -10,19 +10,25 @@
 // weight rows per product, and the block scales combine them in float:
 //
 //   Q4_0, Q5_0, Q8_0   per 32-block:  float(sumi) * (d_w * d_a)
-//   Q4_K               per 256-block: (d yd) float(sum_s sc_s sumi_s) - (dmin yd) float(sum_s m_s bsum_s)
+//   Q4_K               per 256-block: yd (d float(sum_s sc_s sumi_s) - dmin float(sum_s m_s bsum_s))
 //   Q6_K               per 256-block: (d yd) float(sum_h sc_h sumi_h)
 //
 // so each block's integers are ggml's and results differ from its gemv only
-// by float association. The weights are decoded to int8 in registers (Q4_0
-// and Q5_0 to their signed values, Q6_K to q - 32, Q4_K to its unsigned
-// nibbles with the mins through the activation sums).
+// by float association.
 //
-// A workgroup (4 waves) owns 128 weight rows x 64 activation rows; a wave 32
-// weight rows (one per lane, the product's B operand) against the 64
-// activation rows (two A operands), so each decoded weight feeds two
-// products. The activation scales of the block's 64 rows (and, for Q4_K,
-// their sums of 32) are staged in LDS for 128 steps of 32 at a time.
+// Both kernels give a workgroup (4 waves) 128 weight rows x 64 activation
+// rows; a wave 32 weight rows (one per lane, the product's B operand)
+// against the 64 activation rows (two A operands), so each decoded weight
+// feeds two products.
+// - gemm_q_kernel (Q4_0, Q5_0, Q8_0, Q6_K): every lane loads its own weight
+//   row's bytes and its activation rows' bytes into registers, two batches
+//   of steps in flight; the weights are decoded to int8 in registers (Q4_0
+//   and Q5_0 to their signed values, Q6_K to q - 32). The activation scales
+//   of the block's 64 rows are staged in LDS for 128 steps of 32 at a time.
+// - gemm_q4k_kernel (Q4_K): each 256-block's weight and activation bytes
+//   reach LDS through whole-line direct copies, two stages deep; the
+//   sub-block scales are folded into two int8 weight planes and the mins
+//   take one f16 product per block (details at the kernel).
 
 #include "quant.hpp"
 
@@ -85,10 +91,6 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float* x, uint8
 template <uint32_t T>
 struct raw_step;
 template <>
-struct raw_step<qtype_q4_k> {
-    u4 q, a[2];
-};
-template <>
 struct raw_step<qtype_q6_k> {
     uint32_t lw[2][3], hw[2][3], a[2][2][2];  // [half e], [half e][row group][dword]
 };
@@ -109,14 +111,7 @@ template <uint32_t T>
 __device__ __forceinline__ raw_step<T> fetch_step(rsrc wr, rsrc ar, uint32_t wlane, uint32_t arow, uint32_t li,
                                                   uint32_t H, uint32_t k) {
     raw_step<T> x;
-    if constexpr (T == qtype_q4_k) {
-        const uint32_t U = k / 8, s = k % 8;
-        x.q = buffer_load16(wr, wlane + U * 144 + 16 + 32 * (s / 2) + 16 * H);
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            x.a[g] = buffer_load16(ar, (32 * g + li) * arow + U * 292 + 4 + 32 * s + 16 * H);
-        }
-    } else if constexpr (T == qtype_q6_k) {
+    if constexpr (T == qtype_q6_k) {
         const uint32_t U = k / 8, s = k % 8, hf = s / 4, k4 = s % 4;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -148,8 +143,8 @@ __device__ __forceinline__ raw_step<T> fetch_step(rsrc wr, rsrc ar, uint32_t wla
     return x;
 }
 
-// A batch of BS steps' loads and, for the K-quants, its 256-block header
-// (Q4_K: d, dmin, 12 scale bytes; Q6_K: the window of its 16 scales, and d).
+// A batch of BS steps' loads and, for Q6_K, its 256-block header (the window
+// of its 16 scales, and d).
 template <uint32_t T, int BS>
 struct raw_batch {
     raw_step<T> s[BS];
@@ -161,10 +156,8 @@ template <uint32_t T>
 __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
                                                      float* out, uint32_t n, uint32_t rows, uint32_t cols) {
     constexpr bool KQ = k_quant<T>;
-    // Q8_0 pairs: d_a per (step, row); K-quants: yd per (256-block, row), and
-    // for Q4_K the activation sum of each 32-step per (step, row).
+    // Q8_0 pairs: d_a per (step, row); Q6_K: yd per (256-block, row).
     __shared__ __attribute__((aligned(16))) float lds_d[KQ ? gq_k / 8 : gq_k][gq_n];
-    __shared__ __attribute__((aligned(16))) int lds_s[T == qtype_q4_k ? gq_k : 1][gq_n];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -196,29 +189,21 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
         }
     }
     const i16v zero16 = {};
-    // Steps per batch of loads (a Q4_K / Q6_K 256-block is 8 steps).
+    // Steps per batch of loads (a Q6_K 256-block is 8 steps).
     constexpr int BS = KQ ? 2 : 4;
     using batch_t = raw_batch<T, BS>;
     // Per 256-block weight data of this lane's row (K-quants).
-    u4 hdr = {};          // Q4_K: d, dmin, 12 scale bytes; Q6_K: 16 scales
-    float wd = 0.0f, wdmin = 0.0f;
+    u4 hdr = {};  // Q6_K: 16 scales
+    float wd = 0.0f;
 
     for (uint32_t kc = 0; kc < units; kc += gq_k) {
         const uint32_t steps = min(gq_k, units - kc);
-        // ---- stage the chunk's activation scales (and Q4_K sums) ----
+        // ---- stage the chunk's activation scales ----
         __syncthreads();  // the previous chunk's reads are done
         if constexpr (KQ) {
             for (uint32_t e = tid; e < steps / 8 * gq_n; e += 256) {
                 const uint32_t b = e / gq_n, r = e % gq_n;
                 lds_d[b][r] = __builtin_bit_cast(float, ld32(ar, r * arow + (kc / 8 + b) * 292));
-            }
-            if constexpr (T == qtype_q4_k) {
-                for (uint32_t e = tid; e < steps * gq_n; e += 256) {
-                    const uint32_t st = e / gq_n, r = e % gq_n;
-                    const uint32_t k = kc + st;
-                    const uint32_t bs = ld32(ar, r * arow + k / 8 * 292 + 260 + 4 * (k % 8));
-                    lds_s[st][r] = static_cast<int16_t>(bs & 0xFFFF) + static_cast<int16_t>(bs >> 16);
-                }
             }
         } else {
             for (uint32_t e = tid; e < steps * gq_n; e += 256) {
@@ -241,12 +226,8 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
             if constexpr (KQ) {
                 // The 256-block's header (a block spans several batches and each loads it).
                 const uint32_t U = (kc + min(sb, steps - 1)) / 8;
-                if constexpr (T == qtype_q4_k) {
-                    bt.hdr = buffer_load16(wr, wlane + U * 144);
-                } else {
-                    fetch_window(wr, wlane + U * 210 + 192, bt.sw);
-                    bt.d6 = ld16(wr, wlane + U * 210 + 208);
-                }
+                fetch_window(wr, wlane + U * 210 + 192, bt.sw);
+                bt.d6 = ld16(wr, wlane + U * 210 + 208);
             }
         };
         const auto compute_batch = [&](const batch_t& bt, uint32_t sb) __attribute__((always_inline)) {
@@ -255,11 +236,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
             // the scheduler hoists every product of the batch and holds all
             // their results at once.
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (T == qtype_q4_k) {
-                hdr = bt.hdr;
-                wd = half_bits(hdr[0]);
-                wdmin = half_bits(hdr[0] >> 16);
-            } else if constexpr (T == qtype_q6_k) {
+            if constexpr (T == qtype_q6_k) {
                 uint32_t scw[4];
                 realign(bt.sw, wlane + (kc + sb) / 8 * 210 + 192, scw);
                 hdr = u4{scw[0], scw[1], scw[2], scw[3]};
@@ -269,29 +246,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
             for (int b = 0; b < BS; ++b) {
                 const uint32_t st = min(sb + b, steps - 1);
                 const uint32_t k = kc + st;  // 32-wide step
-                if constexpr (T == qtype_q4_k) {
-                    const uint32_t s = k % 8, sh = (s & 1) * 4;
-                    const u4 q = bt.s[b].q;
-                    const i4v bw = {static_cast<int>((q[0] >> sh) & 0x0F0F0F0Fu),
-                                    static_cast<int>((q[1] >> sh) & 0x0F0F0F0Fu),
-                                    static_cast<int>((q[2] >> sh) & 0x0F0F0F0Fu),
-                                    static_cast<int>((q[3] >> sh) & 0x0F0F0F0Fu)};
-                    const auto byte = [&](uint32_t j) { return (hdr[1 + j / 4] >> (8 * (j % 4))) & 0xFFu; };
-                    const int sc = s < 4 ? static_cast<int>(byte(s) & 63)
-                                         : static_cast<int>((byte(s + 4) & 0xF) | ((byte(s - 4) >> 6) << 4));
-#pragma unroll
-                    for (int g = 0; g < 2; ++g) {
-                        const u4 av = bt.s[b].a[g];
-                        const i4v a = {static_cast<int>(av[0]), static_cast<int>(av[1]), static_cast<int>(av[2]),
-                                       static_cast<int>(av[3])};
-                        const i16v cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bw, zero16, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            // |sums| < 2^23: 24-bit multiplies are exact.
-                            isum[g][i] += __mul24(sc, cm[i]);
-                        }
-                    }
-                } else if constexpr (T == qtype_q6_k) {  // two 16-wide halves with their own scales
+                if constexpr (T == qtype_q6_k) {  // two 16-wide halves with their own scales
                     const uint32_t s = k % 8, hf = s / 4, k4 = s % 4;
                     const uint32_t U = k / 8;
 #pragma unroll
@@ -365,34 +320,6 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
                     // Batches of BS steps tile each 8-step 256-block: the batch
                     // that ends one has sb % 8 == 8 - BS.
                     if (b == BS - 1 && sb % 8 == 8 - BS) {
-                        // Q4_K mins: sum_s m_s bsum_s per (activation row, weight
-                        // row) on the f32 matrix cores, K = the 8 sub-blocks;
-                        // every product and sum is an integer below 2^24, so
-                        // exact. A: the activation sums of 32 (lane: row l % 32,
-                        // sub-block 2j + H); B: this lane's weight row's mins.
-                        f16v fmin[2];
-                        if constexpr (T == qtype_q4_k) {
-                            const auto byte = [&](uint32_t j) { return (hdr[1 + j / 4] >> (8 * (j % 4))) & 0xFFu; };
-#pragma unroll
-                            for (int g = 0; g < 2; ++g) {
-#pragma unroll
-                                for (int i = 0; i < 16; ++i) {
-                                    fmin[g][i] = 0.0f;
-                                }
-                            }
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                const uint32_t sub = 2 * j + H;
-                                const int m = sub < 4 ? static_cast<int>(byte(sub + 4) & 63)
-                                                      : static_cast<int>((byte(sub + 4) >> 4) | ((byte(sub) >> 6) << 4));
-#pragma unroll
-                                for (int g = 0; g < 2; ++g) {
-                                    const float am = static_cast<float>(lds_s[st - 7 + sub][32 * g + li]);
-                                    fmin[g] = __builtin_amdgcn_mfma_f32_32x32x2f32(am, static_cast<float>(m), fmin[g],
-                                                                                   0, 0, 0);
-                                }
-                            }
-                        }
                         // The 256-block's float combine.
 #pragma unroll
                         for (int g = 0; g < 2; ++g) {
@@ -400,12 +327,7 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
                             for (int i = 0; i < 16; ++i) {
                                 const uint32_t r = 32 * g + 8 * (i / 4) + 4 * H + i % 4;
                                 const float yd = lds_d[st / 8][r];
-                                if constexpr (T == qtype_q4_k) {
-                                    acc[g][i] += (wd * yd) * static_cast<float>(isum[g][i]) -
-                                                 (wdmin * yd) * fmin[g][i];
-                                } else {
-                                    acc[g][i] += (wd * yd) * static_cast<float>(isum[g][i]);
-                                }
+                                acc[g][i] += (wd * yd) * static_cast<float>(isum[g][i]);
                                 isum[g][i] = 0;
                             }
                         }
@@ -440,6 +362,216 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
     }
 }
 
+// ---- Q4_K through LDS ------------------------------------------------------------------
+//
+// The same tile (4 waves, 128 weight rows x 64 activation rows, a wave's 32
+// weight rows against all 64), but every 256-block reaches the matrix cores
+// through LDS: each wave copies its rows' 144-byte blocks and a quarter of
+// the activation blocks with whole-line direct copies (buffer_load ... lds,
+// 1 KiB per instruction), two stages deep, one barrier per block. The block
+// dots are the reference's integers (S/kernels/dot.hpp:166-201): per
+// 256-block
+//   isum = sum_s sc_s sum_{j in s} q_j a_j,   mins = sum_k m_{k/2} bsum_k
+// over the 16 activation sums of 16, and the float combine
+// yd (d isum - dmin mins). The sub-block scale is
+// folded into the weights so the products accumulate in place: sc = 8 sh + sl
+// (sh, sl < 8), planes q sl and q sh (each below 128, so int8), and isum =
+// sum(a . q sl) + 8 sum(a . q sh). The mins take one f16 product per block:
+// the 16 activation sums of 16 (|b| <= 2032, exact in binary16) against m of
+// their sub-block (each product and the sum of 16 exact in f32).
+
+constexpr uint32_t k4_wave = 32 * 144;                                // one wave's weight rows, one block
+constexpr uint32_t k4_stage = 4 * k4_wave + 64 * 256 + 4 * 512 + 4 * 256;  // weights, qs, bsums, d
+constexpr uint32_t k4_a = 4 * k4_wave, k4_bs = k4_a + 64 * 256, k4_d = k4_bs + 4 * 512;
+
+// Direct copies into LDS at M0 + 16 lane (M0 + 4 lane for the dword form).
+__device__ __forceinline__ void copy16_lds(rsrc r, uint32_t m0, uint32_t voff) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(r), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void copy4_lds(rsrc r, uint32_t m0, uint32_t voff) {
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voff), "s"(r), "{m0}"(m0) : "memory");
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Byte k of x in both 16-bit halves (the other bytes zero).
+__device__ __forceinline__ uint32_t byte_pair(uint32_t x, uint32_t k) {
+    return __builtin_amdgcn_perm(0u, x, 0x0C000C00u | (k << 16) | k);
+}
+__device__ __forceinline__ uint32_t mul_u16x2(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
+                                                          float* out, uint32_t n, uint32_t rows, uint32_t cols) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][k4_stage];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t ln = tid & 63, H = ln >> 5, li = ln & 31;
+    const uint32_t nb = cols / 256;
+    const uint32_t wrow = nb * 144, arow = nb * 292;
+    const uint32_t o0 = blockIdx.x * gq_m + wv * 32;
+    const uint32_t t0 = blockIdx.y * gq_n;
+
+    // The wave's weight rows and the block's activation rows; each copy
+    // reads through a resource rebased to its 256-block, so rows past the
+    // last read zeros.
+    const uint32_t wave_rows = o0 < rows ? min(32u, rows - o0) : 0;
+    const uint8_t* wp = w + static_cast<std::size_t>(min(o0, rows - 1)) * wrow;
+    const uint32_t delta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wp) & 3);
+    const uint8_t* wbase = wp - delta;
+    const uint32_t wbytes = wave_rows * wrow + delta;
+    const uint8_t* abase = act + static_cast<std::size_t>(t0) * arow;
+    const uint32_t abytes = min(gq_n, n - t0) * arow;
+
+    // Per-lane source offsets inside a block. Weights: byte b of the wave's
+    // 32 x 144 image is row b / 144, byte b % 144. Activation qs: row
+    // 16 wv + 4 i + ln / 16, its 16-byte chunk (ln % 16) ^ (row % 16), so a
+    // row's chunks rotate across the LDS banks. bsums: row 16 wv + ln / 2,
+    // half ln % 2 (lanes 0..31). d: row 16 wv + ln (lanes 0..15).
+    uint32_t wo[5], ao[4];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const uint32_t b = 1024 * i + 16 * ln;
+        wo[i] = delta + b / 144 * wrow + b % 144;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = 16 * wv + 4 * i + (ln >> 4);
+        ao[i] = row * arow + 4 + 16 * ((ln & 15) ^ (row & 15));
+    }
+    const uint32_t bo = (16 * wv + (ln >> 1)) * arow + 260 + 16 * (ln & 1);
+    const uint32_t dof = ln < 16 ? (16 * wv + ln) * arow : buffer_oob;
+
+    const uint32_t L0 = lds_address(&lds[0][0]);
+    const auto issue = [&](uint32_t U) __attribute__((always_inline)) {
+        const uint32_t S = L0 + (U & 1) * k4_stage;
+        const rsrc wr = make_rsrc(wbase + U * 144, wave_rows != 0 ? wbytes - U * 144 : 0);
+        const rsrc ar = make_rsrc(abase + U * 292, abytes - U * 292);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            copy16_lds(wr, S + wv * k4_wave + 1024 * i, wo[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            copy16_lds(ar, S + k4_a + (16 * wv + 4 * i) * 256, ao[i]);
+        }
+        copy4_lds(ar, S + k4_d + 256 * wv, dof);
+        if (ln < 32) {
+            copy16_lds(wr, S + wv * k4_wave + 4096, wo[4]);
+            copy16_lds(ar, S + k4_bs + 512 * wv, bo);
+        }
+    };
+
+    float acc[2][16];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            acc[g][i] = 0.0f;
+        }
+    }
+    const i16v zi = {};
+    const f16v zf = {};
+
+    issue(0);
+    for (uint32_t U = 0; U < nb; ++U) {
+        // Block U landed in every wave; every wave is done with block U - 1,
+        // whose stage block U + 1 now takes.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (U + 1 < nb) {
+            issue(U + 1);
+        }
+        const uint8_t* S = lds[U & 1];
+        const uint8_t* Wl = S + wv * k4_wave + li * 144;
+
+        // d, dmin and the 8 (scale, min) pairs of this lane's weight row, as
+        // bytes: sc 0..3, sc 4..7, m 0..3, m 4..7 (ggml's get_scale_min_k4).
+        const u4 hdr = *reinterpret_cast<const u4*>(Wl);
+        const float wd = half_bits(hdr[0] & 0xFFFF), wdmin = half_bits(hdr[0] >> 16);
+        const uint32_t sc[2] = {hdr[1] & 0x3F3F3F3Fu, (hdr[3] & 0x0F0F0F0Fu) | ((hdr[1] >> 2) & 0x30303030u)};
+        const uint32_t mn[2] = {hdr[2] & 0x3F3F3F3Fu, ((hdr[3] >> 4) & 0x0F0F0F0Fu) | ((hdr[2] >> 2) & 0x30303030u)};
+
+        i16v a1[2], a2[2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {  // sub-blocks 2t (low nibbles) and 2t + 1 (high)
+            const u4 qw = *reinterpret_cast<const u4*>(Wl + 16 + 32 * t + 16 * H);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t s = 2 * t + e;
+                const uint32_t sl = byte_pair(sc[s / 4] & 0x07070707u, s % 4);
+                const uint32_t sh = byte_pair((sc[s / 4] >> 3) & 0x07070707u, s % 4);
+                i4v p1, p2;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t nib = (qw[j] >> (4 * e)) & 0x0F0F0F0Fu;
+                    p1[j] = static_cast<int>(mul_u16x2(nib, sl));
+                    p2[j] = static_cast<int>(mul_u16x2(nib, sh));
+                }
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    const uint32_t row = 32 * g + li;
+                    const u4 av = *reinterpret_cast<const u4*>(S + k4_a + row * 256 + 16 * ((2 * s + H) ^ (li & 15)));
+                    const i4v a = {static_cast<int>(av[0]), static_cast<int>(av[1]), static_cast<int>(av[2]),
+                                   static_cast<int>(av[3])};
+                    a1[g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, p1, s == 0 ? zi : a1[g], 0, 0, 0);
+                    a2[g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, p2, s == 0 ? zi : a2[g], 0, 0, 0);
+                }
+            }
+        }
+
+        // mins: B = m of sub-blocks 4H .. 4H + 3, each for its two sums of 16.
+        const uint32_t mh = mn[H];
+        h8 mb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const _Float16 m = static_cast<_Float16>(static_cast<float>((mh >> (8 * j)) & 0xFF));
+            mb[2 * j] = m;
+            mb[2 * j + 1] = m;
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t row = 32 * g + li;
+            const u4 bv = *reinterpret_cast<const u4*>(S + k4_bs + 512 * (row / 16) + 32 * (row % 16) + 16 * H);
+            h8 ab;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ab[2 * j] = static_cast<_Float16>(static_cast<int16_t>(bv[j] & 0xFFFF));
+                ab[2 * j + 1] = static_cast<_Float16>(static_cast<int16_t>(bv[j] >> 16));
+            }
+            const f16v fm = mfma32(ab, mb, zf);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t r0 = 32 * g + 8 * q + 4 * H;
+                const f4 yd = *reinterpret_cast<const f4*>(S + k4_d + 256 * (r0 / 16) + 4 * (r0 % 16));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int i = 4 * q + k;
+                    const int isum = a1[g][i] + (a2[g][i] << 3);
+                    acc[g][i] += yd[k] * (wd * static_cast<float>(isum) - wdmin * fm[i]);
+                }
+            }
+        }
+    }
+
+    const uint32_t o = o0 + li;
+    if (o < rows) {
+        const float bo2 = bias != nullptr ? bias[o] : 0.0f;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t r = t0 + 32 * g + 8 * (i / 4) + 4 * H + i % 4;
+                if (r < n) {
+                    out[static_cast<std::size_t>(r) * rows + o] = acc[g][i] + bo2;
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
@@ -464,7 +596,7 @@ hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* 
         gemm_q_kernel<qtype_q8_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         break;
     case qtype_q4_k:
-        gemm_q_kernel<qtype_q4_k><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        gemm_q4k_kernel<<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         break;
     default:
         gemm_q_kernel<qtype_q6_k><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);

@@ -10,25 +10,26 @@
 // weight rows per product, and the block scales combine them in float:
 //
 //   Q4_0, Q5_0, Q8_0   per 32-block:  float(sumi) * (d_w * d_a)
-//   Q4_K               per 256-block: yd (d float(sum_s sc_s sumi_s) - dmin float(sum_s m_s bsum_s))
-//   Q6_K               per 256-block: (d yd) float(sum_h sc_h sumi_h)
+//   Q4_K               per 256-block: yd (d float(sum_s sc_s sumi_s) - dmin float(sum_k m_k bsum_k))
+//   Q6_K               per 256-block: (d yd) (float(sum_k sc_k sumi_k) - 32 sum_k sc_k bsum_k)
 //
 // so each block's integers are ggml's and results differ from its gemv only
-// by float association.
-//
-// Both kernels give a workgroup (4 waves) 128 weight rows x 64 activation
-// rows; a wave 32 weight rows (one per lane, the product's B operand)
-// against the 64 activation rows (two A operands), so each decoded weight
-// feeds two products.
-// - gemm_q_kernel (Q4_0, Q5_0, Q8_0, Q6_K): every lane loads its own weight
-//   row's bytes and its activation rows' bytes into registers, two batches
-//   of steps in flight; the weights are decoded to int8 in registers (Q4_0
-//   and Q5_0 to their signed values, Q6_K to q - 32). The activation scales
-//   of the block's 64 rows are staged in LDS for 128 steps of 32 at a time.
-// - gemm_q4k_kernel (Q4_K): each 256-block's weight and activation bytes
-//   reach LDS through whole-line direct copies, two stages deep; the
-//   sub-block scales are folded into two int8 weight planes and the mins
-//   take one f16 product per block (details at the kernel).
+// by float association. Three kernels:
+// - gemm_q_kernel (Q4_0, Q5_0, Q8_0): a workgroup (4 waves) owns 128 weight
+//   rows x 64 activation rows; a wave 32 weight rows (one per lane, the
+//   product's B operand) against the 64 activation rows (two A operands).
+//   Every lane loads its own weight row's bytes and its activation rows'
+//   bytes into registers, two batches of steps in flight; the weights are
+//   decoded to signed int8 in registers. The activation scales of the
+//   block's 64 rows are staged in LDS for 128 steps of 32 at a time.
+// - gemm_q4k_kernel (Q4_K): the same tile; each 256-block's weight and
+//   activation bytes reach LDS through whole-line direct copies, two stages
+//   deep; the sub-block scales are folded into two int8 weight planes and the
+//   mins take one f16 product per block.
+// - gemm_q6k_kernel (Q6_K): 64 x 64 per workgroup, 32 x 32 per wave, the
+//   same LDS staging; unsigned quants, the offset through the activation
+//   sums on one f16 product per block.
+// Details at each kernel.
 
 #include "quant.hpp"
 
@@ -48,7 +49,7 @@ constexpr uint32_t gq_m = 128;  // weight rows per workgroup
 constexpr uint32_t gq_n = 64;   // activation rows per workgroup
 constexpr uint32_t gq_k = 128;  // 32-wide steps per staged chunk of activation scales
 
-// Signed bytes from 4-, 5- and 6-bit fields: x - 8, x - 16, x - 32 per byte
+// Signed bytes from 4- and 5-bit fields: x - 8, x - 16 per byte
 // (flip the top bit, then extend it; no carries cross bytes).
 __device__ __forceinline__ uint32_t sext4(uint32_t nib) {
     const uint32_t t = nib ^ 0x08080808u;
@@ -57,10 +58,6 @@ __device__ __forceinline__ uint32_t sext4(uint32_t nib) {
 __device__ __forceinline__ uint32_t sext5(uint32_t x) {
     const uint32_t t = x ^ 0x10101010u;
     return t | ((t & 0x10101010u) * 0x0Eu);
-}
-__device__ __forceinline__ uint32_t sext6(uint32_t x) {
-    const uint32_t t = x ^ 0x20202020u;
-    return t | ((t & 0x20202020u) * 0x06u);
 }
 
 // Activations to ggml's layout, one lane per 32 values (the 8 lanes of a
@@ -91,10 +88,6 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float* x, uint8
 template <uint32_t T>
 struct raw_step;
 template <>
-struct raw_step<qtype_q6_k> {
-    uint32_t lw[2][3], hw[2][3], a[2][2][2];  // [half e], [half e][row group][dword]
-};
-template <>
 struct raw_step<qtype_q8_0> {
     uint32_t d, qw[5], aw[2][5];
 };
@@ -111,20 +104,7 @@ template <uint32_t T>
 __device__ __forceinline__ raw_step<T> fetch_step(rsrc wr, rsrc ar, uint32_t wlane, uint32_t arow, uint32_t li,
                                                   uint32_t H, uint32_t k) {
     raw_step<T> x;
-    if constexpr (T == qtype_q6_k) {
-        const uint32_t U = k / 8, s = k % 8, hf = s / 4, k4 = s % 4;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            fetch_window(wr, wlane + U * 210 + 64 * hf + 32 * (k4 & 1) + 16 * e + 8 * H, x.lw[e]);
-            fetch_window(wr, wlane + U * 210 + 128 + 32 * hf + 16 * e + 8 * H, x.hw[e]);
-#pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const uint32_t aoff = (32 * g + li) * arow + U * 292 + 4 + 32 * s + 16 * e + 8 * H;
-                x.a[e][g][0] = ld32(ar, aoff);
-                x.a[e][g][1] = ld32(ar, aoff + 4);
-            }
-        }
-    } else {
+    {
         const uint32_t b0 = wlane + k * block_bytes<T>;
         x.d = ld16(wr, b0);
         if constexpr (T == qtype_q8_0) {
@@ -143,28 +123,24 @@ __device__ __forceinline__ raw_step<T> fetch_step(rsrc wr, rsrc ar, uint32_t wla
     return x;
 }
 
-// A batch of BS steps' loads and, for Q6_K, its 256-block header (the window
-// of its 16 scales, and d).
+// A batch of BS steps' loads.
 template <uint32_t T, int BS>
 struct raw_batch {
     raw_step<T> s[BS];
-    u4 hdr;
-    uint32_t sw[5], d6;
 };
 
 template <uint32_t T>
 __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
                                                      float* out, uint32_t n, uint32_t rows, uint32_t cols) {
-    constexpr bool KQ = k_quant<T>;
-    // Q8_0 pairs: d_a per (step, row); Q6_K: yd per (256-block, row).
-    __shared__ __attribute__((aligned(16))) float lds_d[KQ ? gq_k / 8 : gq_k][gq_n];
+    // The activation scales d_a per (step, row).
+    __shared__ __attribute__((aligned(16))) float lds_d[gq_k][gq_n];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t ln = tid & 63, H = ln >> 5, li = ln & 31;
     const uint32_t units = cols / 32;
-    const uint32_t wrow = cols / (KQ ? 256 : 32) * block_bytes<T>;
-    const uint32_t arow = KQ ? units / 8 * 292 : units * 34;
+    const uint32_t wrow = units * block_bytes<T>;
+    const uint32_t arow = units * 34;
     const uint32_t o0 = blockIdx.x * gq_m + wv * 32;  // the wave's first weight row
     const uint32_t t0 = blockIdx.y * gq_n;            // the block's first activation row
 
@@ -179,55 +155,35 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
     const rsrc ar = make_rsrc(act + static_cast<std::size_t>(t0) * arow, min(gq_n, n - t0) * arow);
 
     float acc[2][16];
-    int isum[2][16];
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             acc[g][i] = 0.0f;
-            isum[g][i] = 0;
         }
     }
     const i16v zero16 = {};
-    // Steps per batch of loads (a Q6_K 256-block is 8 steps).
-    constexpr int BS = KQ ? 2 : 4;
+    constexpr int BS = 4;  // steps per batch of loads
     using batch_t = raw_batch<T, BS>;
-    // Per 256-block weight data of this lane's row (K-quants).
-    u4 hdr = {};  // Q6_K: 16 scales
-    float wd = 0.0f;
 
     for (uint32_t kc = 0; kc < units; kc += gq_k) {
         const uint32_t steps = min(gq_k, units - kc);
         // ---- stage the chunk's activation scales ----
         __syncthreads();  // the previous chunk's reads are done
-        if constexpr (KQ) {
-            for (uint32_t e = tid; e < steps / 8 * gq_n; e += 256) {
-                const uint32_t b = e / gq_n, r = e % gq_n;
-                lds_d[b][r] = __builtin_bit_cast(float, ld32(ar, r * arow + (kc / 8 + b) * 292));
-            }
-        } else {
-            for (uint32_t e = tid; e < steps * gq_n; e += 256) {
-                const uint32_t st = e / gq_n, r = e % gq_n;
-                lds_d[st][r] = half_bits(ld16(ar, r * arow + (kc + st) * 34));
-            }
+        for (uint32_t e = tid; e < steps * gq_n; e += 256) {
+            const uint32_t st = e / gq_n, r = e % gq_n;
+            lds_d[st][r] = half_bits(ld16(ar, r * arow + (kc + st) * 34));
         }
         __syncthreads();
 
         // Steps go in batches of BS, two batches in flight: batch i + 1's
         // loads are issued before batch i's products, so a wave's memory
         // waits overlap its own work. Loads past the chunk's last step read a
-        // valid step whose products are dropped (Q4_0 / Q5_0 / Q8_0; the
-        // K-quant chunks are whole 256-blocks).
+        // valid step whose products are dropped.
         const auto fetch_batch = [&](batch_t& bt, uint32_t sb) __attribute__((always_inline)) {
 #pragma unroll
             for (int b = 0; b < BS; ++b) {
                 bt.s[b] = fetch_step<T>(wr, ar, wlane, arow, li, H, kc + min(sb + b, steps - 1));
-            }
-            if constexpr (KQ) {
-                // The 256-block's header (a block spans several batches and each loads it).
-                const uint32_t U = (kc + min(sb, steps - 1)) / 8;
-                fetch_window(wr, wlane + U * 210 + 192, bt.sw);
-                bt.d6 = ld16(wr, wlane + U * 210 + 208);
             }
         };
         const auto compute_batch = [&](const batch_t& bt, uint32_t sb) __attribute__((always_inline)) {
@@ -236,46 +192,11 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
             // the scheduler hoists every product of the batch and holds all
             // their results at once.
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (T == qtype_q6_k) {
-                uint32_t scw[4];
-                realign(bt.sw, wlane + (kc + sb) / 8 * 210 + 192, scw);
-                hdr = u4{scw[0], scw[1], scw[2], scw[3]};
-                wd = half_bits(bt.d6);
-            }
 #pragma unroll
             for (int b = 0; b < BS; ++b) {
                 const uint32_t st = min(sb + b, steps - 1);
                 const uint32_t k = kc + st;  // 32-wide step
-                if constexpr (T == qtype_q6_k) {  // two 16-wide halves with their own scales
-                    const uint32_t s = k % 8, hf = s / 4, k4 = s % 4;
-                    const uint32_t U = k / 8;
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        uint32_t lo[2], hi[2];
-                        realign(bt.s[b].lw[e], wlane + U * 210 + 64 * hf + 32 * (k4 & 1) + 16 * e + 8 * H, lo);
-                        realign(bt.s[b].hw[e], wlane + U * 210 + 128 + 32 * hf + 16 * e + 8 * H, hi);
-                        uint32_t q[2];
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            q[j] = sext6(((lo[j] >> (4 * (k4 >> 1))) & 0x0F0F0F0Fu) |
-                                         (((hi[j] >> (2 * k4)) & 0x03030303u) << 4));
-                        }
-                        const long bw = static_cast<long>((static_cast<uint64_t>(q[1]) << 32) | q[0]);
-                        const uint32_t si = 8 * hf + 2 * k4 + e;  // this half's scale
-                        const int sc = static_cast<int8_t>((hdr[si / 4] >> (8 * (si % 4))) & 0xFF);
-#pragma unroll
-                        for (int g = 0; g < 2; ++g) {
-                            const long a = static_cast<long>((static_cast<uint64_t>(bt.s[b].a[e][g][1]) << 32) |
-                                                             bt.s[b].a[e][g][0]);
-                            const i16v cm = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, bw, zero16, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 16; ++i) {
-                                isum[g][i] += __mul24(sc, cm[i]);
-                            }
-                        }
-                    }
-                } else {
-                    // Q4_0 / Q5_0 / Q8_0 block k: 16 signed weights for this lane half.
+                {  // block k: 16 signed weights for this lane half
                     const uint32_t b0 = wlane + k * block_bytes<T>;
                     // A step past the chunk's last (the batch's tail) adds zeros.
                     const float dw = sb + b < steps ? half_bits(bt.s[b].d) : 0.0f;
@@ -316,23 +237,6 @@ __global__ __launch_bounds__(256) void gemm_q_kernel(const uint8_t* w, const uin
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (KQ) {
-                    // Batches of BS steps tile each 8-step 256-block: the batch
-                    // that ends one has sb % 8 == 8 - BS.
-                    if (b == BS - 1 && sb % 8 == 8 - BS) {
-                        // The 256-block's float combine.
-#pragma unroll
-                        for (int g = 0; g < 2; ++g) {
-#pragma unroll
-                            for (int i = 0; i < 16; ++i) {
-                                const uint32_t r = 32 * g + 8 * (i / 4) + 4 * H + i % 4;
-                                const float yd = lds_d[st / 8][r];
-                                acc[g][i] += (wd * yd) * static_cast<float>(isum[g][i]);
-                                isum[g][i] = 0;
-                            }
-                        }
-                    }
-                }
             }
         };
         batch_t ba, bb;
@@ -421,7 +325,9 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t* w, cons
     const uint8_t* wp = w + static_cast<std::size_t>(min(o0, rows - 1)) * wrow;
     const uint32_t delta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wp) & 3);
     const uint8_t* wbase = wp - delta;
-    const uint32_t wbytes = wave_rows * wrow + delta;
+    // Whole dwords: a copy's range check is per dword, and the last row may
+    // end inside one (which never crosses a page).
+    const uint32_t wbytes = (wave_rows * wrow + delta + 3) & ~3u;
     const uint8_t* abase = act + static_cast<std::size_t>(t0) * arow;
     const uint32_t abytes = min(gq_n, n - t0) * arow;
 
@@ -572,6 +478,233 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(const uint8_t* w, cons
     }
 }
 
+// ---- Q6_K through LDS ------------------------------------------------------------------
+//
+// A workgroup (4 waves) owns 64 weight rows x 64 activation rows; a wave 32
+// x 32 (weight half wv % 2, activation half wv / 2), so a shape like
+// ffn_down (4096 rows) still fills every SIMD twice. Each 256-block reaches
+// LDS through direct copies: a weight row's 210-byte block as the 240-byte
+// window from the dword at or before it (read back realigned by
+// v_alignbyte), the activation blocks as in the Q4_K kernel. The block dot
+// is the reference's (S/kernels/dot.hpp:203-236): per sub-block of 16,
+// sc_k sum (q - 32) a. The quants are used unsigned (q, 0..63, on the int8
+// matrix cores; each sub-block's sum scaled by sc_k in 24-bit integer
+// multiply-adds) and the offset comes out through the activation sums of 16:
+//   isum = sum_k sc_k sum_{j in k} q_j a_j - 32 sum_k sc_k bsum_k
+// the second sum on one f16 product per block (|sc| <= 128, |bsum| <= 2032:
+// exact in binary16, each product and the sum of 16 exact in f32).
+
+// A row's window: 15 chunks, 210 bytes from any dword start plus one chunk
+// of padding, so that rows 60 dwords apart hit distinct LDS banks.
+constexpr uint32_t k6_win = 240;
+constexpr uint32_t k6_a = 64 * k6_win, k6_bs = k6_a + 64 * 256, k6_d = k6_bs + 4 * 512;
+constexpr uint32_t k6_stage = k6_d + 4 * 256;
+
+// 8 bytes at byte o (0..3) of the 12 at p (p 4-aligned).
+__device__ __forceinline__ uint64_t lds_bytes8(const uint8_t* p, uint32_t o) {
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(p);
+    const uint32_t a = d[0], b = d[1], c = d[2];
+    return (static_cast<uint64_t>(__builtin_amdgcn_alignbyte(c, b, o)) << 32) | __builtin_amdgcn_alignbyte(b, a, o);
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
+                                                          float* out, uint32_t n, uint32_t rows, uint32_t cols) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][k6_stage];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t ln = tid & 63, H = ln >> 5, li = ln & 31;
+    const uint32_t wh = wv & 1, ag = wv >> 1;
+    const uint32_t nb = cols / 256;
+    const uint32_t wrow = nb * 210, arow = nb * 292;
+    const uint32_t r0 = blockIdx.x * 64;  // the block's first weight row (< rows)
+    const uint32_t t0 = blockIdx.y * gq_n;
+
+    const uint8_t* wp = w + static_cast<std::size_t>(r0) * wrow;
+    const uint32_t delta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wp) & 3);
+    const uint8_t* wbase = wp - delta;
+    // Whole dwords: a copy's range check is per dword, and the last row's
+    // block may end inside one (which never crosses a page).
+    const uint32_t wbytes = (min(64u, rows - r0) * wrow + delta + 3) & ~3u;
+    const uint8_t* abase = act + static_cast<std::size_t>(t0) * arow;
+    const uint32_t abytes = min(gq_n, n - t0) * arow;
+
+    // Block U of row r starts at byte X_r + 210 U of the weight resource, X_r
+    // = delta + r wrow. Its window starts at the dword at or before that,
+    // (X_r + 2 (U % 2)) rounded down plus 210 U - 2 (U % 2) (a multiple of
+    // 4), so each copy reads through a resource rebased by the latter, from
+    // one of two per-lane offsets by the parity of U. Wave wv copies rows
+    // 16 wv .. 16 wv + 15: chunk ch = 64 i + ln of its 240, row 16 wv + ch /
+    // 15, chunk ch % 15 (lanes 0..47 of the fourth copy).
+    uint32_t wo[2][4], ao[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t ch = 64 * i + ln;
+        const uint32_t x = delta + (16 * wv + ch / 15) * wrow;
+        wo[0][i] = (x & ~3u) + 16 * (ch % 15);
+        wo[1][i] = ((x + 2) & ~3u) + 16 * (ch % 15);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = 16 * wv + 4 * i + (ln >> 4);
+        ao[i] = row * arow + 4 + 16 * ((ln & 15) ^ (row & 15));
+    }
+    const uint32_t bo = (16 * wv + (ln >> 1)) * arow + 260 + 16 * (ln & 1);
+    const uint32_t dof = ln < 16 ? (16 * wv + ln) * arow : buffer_oob;
+
+    const uint32_t L0 = lds_address(&lds[0][0]);
+    const auto issue = [&](uint32_t U) __attribute__((always_inline)) {
+        const uint32_t S = L0 + (U & 1) * k6_stage;
+        const uint32_t shift = 210 * U - 2 * (U & 1);
+        const rsrc wr = make_rsrc(wbase + shift, wbytes - shift);
+        const rsrc ar = make_rsrc(abase + U * 292, abytes - U * 292);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            copy16_lds(wr, S + 16 * k6_win * wv + 1024 * i, (U & 1) ? wo[1][i] : wo[0][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            copy16_lds(ar, S + k6_a + (16 * wv + 4 * i) * 256, ao[i]);
+        }
+        copy4_lds(ar, S + k6_d + 256 * wv, dof);
+        if (ln < 48) {
+            copy16_lds(wr, S + 16 * k6_win * wv + 3072, (U & 1) ? wo[1][3] : wo[0][3]);
+        }
+        if (ln < 32) {
+            copy16_lds(ar, S + k6_bs + 512 * wv, bo);
+        }
+    };
+
+    float acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        acc[i] = 0.0f;
+    }
+    const f16v zf = {};
+    const uint32_t wrow_l = 32 * wh + li;  // this lane's weight row in the block
+    const uint32_t arow_l = 32 * ag + li;  // this lane's activation row (A operand)
+    const uint32_t xl = delta + wrow_l * wrow;
+
+    issue(0);
+    for (uint32_t U = 0; U < nb; ++U) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (U + 1 < nb) {
+            issue(U + 1);
+        }
+        const uint8_t* S = lds[U & 1];
+        const uint8_t* RB = S + wrow_l * k6_win;  // the window; the block starts at byte o
+        const uint32_t o = (xl + 2 * (U & 1)) & 3;
+
+        // 16 signed scales and d.
+        const u4 s4 = *reinterpret_cast<const u4*>(RB + 192);
+        const uint32_t s5 = *reinterpret_cast<const uint32_t*>(RB + 208);
+        const uint32_t s6 = *reinterpret_cast<const uint32_t*>(RB + 212);
+        const uint32_t sc[4] = {__builtin_amdgcn_alignbyte(s4[1], s4[0], o), __builtin_amdgcn_alignbyte(s4[2], s4[1], o),
+                                __builtin_amdgcn_alignbyte(s4[3], s4[2], o), __builtin_amdgcn_alignbyte(s5, s4[3], o)};
+        const float wd = half_bits(__builtin_amdgcn_alignbyte(s6, s5, o) & 0xFFFF);
+
+        // Four groups (hf, kq) of four products (kh, e) each: a group's
+        // products are issued before the previous group's results are scaled,
+        // so the matrix cores run under the integer multiply-adds.
+        int isum[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            isum[i] = 0;
+        }
+        i16v cm[2][4];
+        int sck[2][4];
+        const auto scale_group = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    // |sums| < 2^17 and |sc| <= 128: 24-bit multiplies are
+                    // exact. The empty asm keeps one multiply-add per product
+                    // (else the adds are regrouped into separate multiplies
+                    // and three-input adds).
+                    int v = __mul24(sck[t & 1][j], cm[t & 1][j][i]) + isum[i];
+                    asm volatile("" : "+v"(v));
+                    isum[i] = v;
+                }
+            }
+        };
+        uint64_t qh[2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int hf = t / 2, kq = t % 2;
+            if (kq == 0) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    qh[e] = lds_bytes8(RB + 128 + 32 * hf + 16 * e + 8 * H, o);
+                }
+            }
+            uint64_t ql[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                ql[e] = lds_bytes8(RB + 64 * hf + 32 * kq + 16 * e + 8 * H, o);
+            }
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                const int k4 = 2 * kh + kq, s = 4 * hf + k4;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const uint64_t lo = (ql[e] >> (4 * kh)) & 0x0F0F0F0F0F0F0F0Full;
+                    const uint64_t hi = k4 < 3 ? (qh[e] << (4 - 2 * k4)) & 0x3030303030303030ull
+                                               : (qh[e] >> 2) & 0x3030303030303030ull;
+                    const long bw = static_cast<long>(lo | hi);
+                    const long a = *reinterpret_cast<const long*>(S + k6_a + arow_l * 256 +
+                                                                  16 * ((2 * s + e) ^ (li & 15)) + 8 * H);
+                    cm[t & 1][2 * kh + e] = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, bw, i16v{}, 0, 0, 0);
+                    const uint32_t k = 2 * s + e;  // sub-block of 16
+                    sck[t & 1][2 * kh + e] = static_cast<int8_t>((sc[k / 4] >> (8 * (k % 4))) & 0xFF);
+                }
+            }
+            if (t > 0) {
+                scale_group(t - 1);
+            }
+        }
+        scale_group(3);
+
+        // The offset term: A = the activation sums of 16, B = sc, both for
+        // k = 8H .. 8H + 7.
+        const u4 bv = *reinterpret_cast<const u4*>(S + k6_bs + 512 * (arow_l / 16) + 32 * (arow_l % 16) + 16 * H);
+        h8 ab, sb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ab[2 * j] = static_cast<_Float16>(static_cast<int16_t>(bv[j] & 0xFFFF));
+            ab[2 * j + 1] = static_cast<_Float16>(static_cast<int16_t>(bv[j] >> 16));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            sb[j] = static_cast<_Float16>(static_cast<int8_t>((sc[2 * H + j / 4] >> (8 * (j % 4))) & 0xFF));
+        }
+        const f16v cf = mfma32(ab, sb, zf);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t rq = 32 * ag + 8 * q + 4 * H;
+            const f4 yd = *reinterpret_cast<const f4*>(S + k6_d + 256 * (rq / 16) + 4 * (rq % 16));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = 4 * q + k;
+                acc[i] += (wd * yd[k]) * (static_cast<float>(isum[i]) - 32.0f * cf[i]);
+            }
+        }
+    }
+
+    const uint32_t o = r0 + wrow_l;
+    if (o < rows) {
+        const float bo2 = bias != nullptr ? bias[o] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t r = t0 + 32 * ag + 8 * (i / 4) + 4 * H + i % 4;
+            if (r < n) {
+                out[static_cast<std::size_t>(r) * rows + o] = acc[i] + bo2;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
@@ -599,7 +732,7 @@ hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* 
         gemm_q4k_kernel<<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         break;
     default:
-        gemm_q_kernel<qtype_q6_k><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        gemm_q6k_kernel<<<dim3((rows + 63) / 64, grid.y), 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         break;
     }
     return hipGetLastError();

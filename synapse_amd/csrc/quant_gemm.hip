@@ -705,6 +705,169 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(const uint8_t* w, cons
     }
 }
 
+
+// ---- Q8_0 through LDS ------------------------------------------------------------------
+//
+// The Q4_K tile (4 waves, 128 weight rows x 64 activation rows, a wave's 32
+// against all 64) over stages of four 34-byte blocks (128 weights). A row's
+// 136 bytes of a stage start at the same byte of a dword in every stage, so
+// each row is copied as the 144-byte window from the dword at or before it
+// (rows 36 dwords apart in LDS: distinct banks) and read back realigned by
+// v_alignbyte. The stage's activation scales (64 rows x 4 blocks, one per
+// thread) are loaded into registers with the copies and written to LDS as
+// f32 before the stage's barrier. Per block, the reference's
+// float(sumi) (d_w d_a) (S/kernels/dot.hpp, the Q8_0 block kernel).
+
+constexpr uint32_t k8_win = 144;
+constexpr uint32_t k8_a = 128 * k8_win, k8_da = k8_a + 64 * k8_win;
+constexpr uint32_t k8_stage = k8_da + 4 * 64 * 4;
+
+// 16 bytes at byte o (0..3) of the 20 at p (p 4-aligned).
+__device__ __forceinline__ i4v lds_bytes16(const uint8_t* p, uint32_t o) {
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(p);
+    uint32_t w5[5];
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        w5[k] = d[k];
+    }
+    return i4v{static_cast<int>(__builtin_amdgcn_alignbyte(w5[1], w5[0], o)),
+               static_cast<int>(__builtin_amdgcn_alignbyte(w5[2], w5[1], o)),
+               static_cast<int>(__builtin_amdgcn_alignbyte(w5[3], w5[2], o)),
+               static_cast<int>(__builtin_amdgcn_alignbyte(w5[4], w5[3], o))};
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_q80_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
+                                                          float* out, uint32_t n, uint32_t rows, uint32_t cols) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][k8_stage];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t ln = tid & 63, H = ln >> 5, li = ln & 31;
+    const uint32_t nst = cols / 128;  // stages of 4 blocks
+    const uint32_t wrow = cols / 32 * 34, arow = wrow;
+    const uint32_t o0 = blockIdx.x * gq_m + wv * 32;
+    const uint32_t t0 = blockIdx.y * gq_n;
+
+    // The wave's weight rows and the block's activation rows, each through a
+    // resource from the dword at or before its first byte, rebased per stage;
+    // whole dwords, as a copy's range check is per dword.
+    const uint32_t wave_rows = o0 < rows ? min(32u, rows - o0) : 0;
+    const uint8_t* wp = w + static_cast<std::size_t>(min(o0, rows - 1)) * wrow;
+    const uint32_t delta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wp) & 3);
+    const uint8_t* wbase = wp - delta;
+    const uint32_t wbytes = (wave_rows * wrow + delta + 3) & ~3u;
+    const uint8_t* ap = act + static_cast<std::size_t>(t0) * arow;
+    const uint32_t adelta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ap) & 3);
+    const uint8_t* abase = ap - adelta;
+    const uint32_t abytes = (min(gq_n, n - t0) * arow + adelta + 3) & ~3u;
+
+    // Copies: wave wv's 32 weight rows, chunk ch = 64 i + ln of its 288 (row
+    // ch / 9, chunk ch % 9; lanes 0..31 of the fifth copy), and activation
+    // rows 16 wv .. 16 wv + 15, chunk ch of their 144 (lanes 0..15 of the
+    // third). The d_a of row tid % 64, block tid / 64.
+    uint32_t wo[5], ao[3];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const uint32_t ch = 64 * i + ln;
+        wo[i] = ((delta + ch / 9 * wrow) & ~3u) + 16 * (ch % 9);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const uint32_t ch = 64 * i + ln;
+        ao[i] = ((adelta + (16 * wv + ch / 9) * arow) & ~3u) + 16 * (ch % 9);
+    }
+    const uint32_t dao = adelta + (tid & 63) * arow + (tid >> 6) * 34;
+
+    const uint32_t L0 = lds_address(&lds[0][0]);
+    uint32_t dah = 0;
+    const auto issue = [&](uint32_t U) __attribute__((always_inline)) {
+        const uint32_t S = L0 + (U & 1) * k8_stage;
+        const rsrc wr = make_rsrc(wbase + U * 136, wave_rows != 0 ? wbytes - U * 136 : 0);
+        const rsrc ar = make_rsrc(abase + U * 136, abytes - U * 136);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            copy16_lds(wr, S + 32 * k8_win * wv + 1024 * i, wo[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            copy16_lds(ar, S + k8_a + 16 * k8_win * wv + 1024 * i, ao[i]);
+        }
+        if (ln < 32) {
+            copy16_lds(wr, S + 32 * k8_win * wv + 4096, wo[4]);
+        }
+        if (ln < 16) {
+            copy16_lds(ar, S + k8_a + 16 * k8_win * wv + 2048, ao[2]);
+        }
+        dah = ld16(ar, dao);
+    };
+
+    float acc[2][16];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            acc[g][i] = 0.0f;
+        }
+    }
+    // Byte of a dword where this lane's weight row and activation rows start.
+    const uint32_t ow = (delta + li * wrow) & 3;
+    uint32_t oa[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        oa[g] = (adelta + (32 * g + li) * arow) & 3;
+    }
+
+    issue(0);
+    for (uint32_t U = 0; U < nst; ++U) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        reinterpret_cast<float*>(lds[U & 1] + k8_da)[tid] = half_bits(dah);  // [block tid / 64][row tid % 64]
+        lds_barrier();
+        if (U + 1 < nst) {
+            issue(U + 1);
+        }
+        const uint8_t* S = lds[U & 1];
+        const uint8_t* WR = S + (32 * wv + li) * k8_win;
+        const float* da = reinterpret_cast<const float*>(S + k8_da);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t xd = ow + 34 * b;  // d_w, then 16 bytes for this lane half
+            const uint32_t* dwp = reinterpret_cast<const uint32_t*>(WR + (xd & ~3u));
+            const float dw = half_bits(__builtin_amdgcn_alignbyte(dwp[1], dwp[0], xd & 3) & 0xFFFF);
+            const uint32_t xq = xd + 2 + 16 * H;
+            const i4v q = lds_bytes16(WR + (xq & ~3u), xq & 3);
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const uint32_t xa = oa[g] + 34 * b + 2 + 16 * H;
+                const i4v a = lds_bytes16(S + k8_a + (32 * g + li) * k8_win + (xa & ~3u), xa & 3);
+                const i16v cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i16v{}, 0, 0, 0);
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    const f4 d4 = *reinterpret_cast<const f4*>(da + 64 * b + 32 * g + 8 * qd + 4 * H);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        acc[g][4 * qd + k] += static_cast<float>(cm[4 * qd + k]) * (dw * d4[k]);
+                    }
+                }
+            }
+        }
+    }
+
+    const uint32_t o = o0 + li;
+    if (o < rows) {
+        const float bo = bias != nullptr ? bias[o] : 0.0f;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t r = t0 + 32 * g + 8 * (i / 4) + 4 * H + i % 4;
+                if (r < n) {
+                    out[static_cast<std::size_t>(r) * rows + o] = acc[g][i] + bo;
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
@@ -726,7 +889,11 @@ hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* 
         gemm_q_kernel<qtype_q5_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         break;
     case qtype_q8_0:
-        gemm_q_kernel<qtype_q8_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        if (cols % 128 == 0) {
+            gemm_q80_kernel<<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        } else {
+            gemm_q_kernel<qtype_q8_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        }
         break;
     case qtype_q4_k:
         gemm_q4k_kernel<<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);

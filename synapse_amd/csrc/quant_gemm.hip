@@ -709,18 +709,26 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(const uint8_t* w, cons
 // ---- Q8_0 through LDS ------------------------------------------------------------------
 //
 // The Q4_K tile (4 waves, 128 weight rows x 64 activation rows, a wave's 32
-// against all 64) over stages of four 34-byte blocks (128 weights). A row's
-// 136 bytes of a stage start at the same byte of a dword in every stage, so
-// each row is copied as the 144-byte window from the dword at or before it
-// (rows 36 dwords apart in LDS: distinct banks) and read back realigned by
-// v_alignbyte. The stage's activation scales (64 rows x 4 blocks, one per
+// against all 64) over stages of NB 34-byte blocks (launched with NB = 2: 32
+// KB of LDS, so the whole grid of a 14336-row product is resident at once;
+// NB = 4 measured 4-5 % slower). A row's 34 NB bytes of a stage start at the
+// same byte of a dword in every stage, so each row is copied as a window of
+// whole chunks from the dword at or before it (rows 20 or 36 dwords apart in
+// LDS: distinct banks) and read back realigned by v_alignbyte. The stage's activation scales (64 rows x 4 blocks, one per
 // thread) are loaded into registers with the copies and written to LDS as
 // f32 before the stage's barrier. Per block, the reference's
 // float(sumi) (d_w d_a) (S/kernels/dot.hpp, the Q8_0 block kernel).
 
-constexpr uint32_t k8_win = 144;
-constexpr uint32_t k8_a = 128 * k8_win, k8_da = k8_a + 64 * k8_win;
-constexpr uint32_t k8_stage = k8_da + 4 * 64 * 4;
+// NB blocks per stage: a row's 34 NB bytes from any dword start, in a window
+// of 16-byte chunks.
+template <int NB>
+constexpr uint32_t k8_win = NB == 4 ? 144 : 80;
+template <int NB>
+constexpr uint32_t k8_a = 128 * k8_win<NB>;
+template <int NB>
+constexpr uint32_t k8_da = k8_a<NB> + 64 * k8_win<NB>;
+template <int NB>
+constexpr uint32_t k8_stage = k8_da<NB> + NB * 64 * 4;
 
 // 16 bytes at byte o (0..3) of the 20 at p (p 4-aligned).
 __device__ __forceinline__ i4v lds_bytes16(const uint8_t* p, uint32_t o) {
@@ -736,14 +744,19 @@ __device__ __forceinline__ i4v lds_bytes16(const uint8_t* p, uint32_t o) {
                static_cast<int>(__builtin_amdgcn_alignbyte(w5[4], w5[3], o))};
 }
 
-__global__ __launch_bounds__(256, 2) void gemm_q80_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
-                                                          float* out, uint32_t n, uint32_t rows, uint32_t cols) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][k8_stage];
+template <int NB>
+__global__ __launch_bounds__(256, NB == 4 ? 2 : 4) void gemm_q80_kernel(const uint8_t* w, const uint8_t* act,
+                                                                        const float* bias, float* out, uint32_t n,
+                                                                        uint32_t rows, uint32_t cols) {
+    constexpr uint32_t WIN = k8_win<NB>, CH = WIN / 16, SB = 34 * NB;  // chunks per row, bytes per row-stage
+    constexpr uint32_t KA = k8_a<NB>, KD = k8_da<NB>, KS = k8_stage<NB>;
+    constexpr int NW = (32 * CH + 63) / 64, NA = (16 * CH + 63) / 64;  // copies per wave
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][KS];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t ln = tid & 63, H = ln >> 5, li = ln & 31;
-    const uint32_t nst = cols / 128;  // stages of 4 blocks
+    const uint32_t nst = cols / (32 * NB);
     const uint32_t wrow = cols / 32 * 34, arow = wrow;
     const uint32_t o0 = blockIdx.x * gq_m + wv * 32;
     const uint32_t t0 = blockIdx.y * gq_n;
@@ -765,40 +778,40 @@ __global__ __launch_bounds__(256, 2) void gemm_q80_kernel(const uint8_t* w, cons
     // ch / 9, chunk ch % 9; lanes 0..31 of the fifth copy), and activation
     // rows 16 wv .. 16 wv + 15, chunk ch of their 144 (lanes 0..15 of the
     // third). The d_a of row tid % 64, block tid / 64.
-    uint32_t wo[5], ao[3];
+    uint32_t wo[NW], ao[NA];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
+    for (int i = 0; i < NW; ++i) {
         const uint32_t ch = 64 * i + ln;
-        wo[i] = ((delta + ch / 9 * wrow) & ~3u) + 16 * (ch % 9);
+        wo[i] = ((delta + ch / CH * wrow) & ~3u) + 16 * (ch % CH);
     }
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < NA; ++i) {
         const uint32_t ch = 64 * i + ln;
-        ao[i] = ((adelta + (16 * wv + ch / 9) * arow) & ~3u) + 16 * (ch % 9);
+        ao[i] = ((adelta + (16 * wv + ch / CH) * arow) & ~3u) + 16 * (ch % CH);
     }
     const uint32_t dao = adelta + (tid & 63) * arow + (tid >> 6) * 34;
 
     const uint32_t L0 = lds_address(&lds[0][0]);
     uint32_t dah = 0;
     const auto issue = [&](uint32_t U) __attribute__((always_inline)) {
-        const uint32_t S = L0 + (U & 1) * k8_stage;
-        const rsrc wr = make_rsrc(wbase + U * 136, wave_rows != 0 ? wbytes - U * 136 : 0);
-        const rsrc ar = make_rsrc(abase + U * 136, abytes - U * 136);
+        const uint32_t S = L0 + (U & 1) * KS;
+        const rsrc wr = make_rsrc(wbase + U * SB, wave_rows != 0 ? wbytes - U * SB : 0);
+        const rsrc ar = make_rsrc(abase + U * SB, abytes - U * SB);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            copy16_lds(wr, S + 32 * k8_win * wv + 1024 * i, wo[i]);
+        for (int i = 0; i < NW; ++i) {
+            if (64 * i + 64 <= 32 * CH || ln < 32 * CH - 64 * i) {
+                copy16_lds(wr, S + 32 * WIN * wv + 1024 * i, wo[i]);
+            }
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            copy16_lds(ar, S + k8_a + 16 * k8_win * wv + 1024 * i, ao[i]);
+        for (int i = 0; i < NA; ++i) {
+            if (64 * i + 64 <= 16 * CH || ln < 16 * CH - 64 * i) {
+                copy16_lds(ar, S + KA + 16 * WIN * wv + 1024 * i, ao[i]);
+            }
         }
-        if (ln < 32) {
-            copy16_lds(wr, S + 32 * k8_win * wv + 4096, wo[4]);
+        if (tid < 64 * NB) {
+            dah = ld16(ar, dao);
         }
-        if (ln < 16) {
-            copy16_lds(ar, S + k8_a + 16 * k8_win * wv + 2048, ao[2]);
-        }
-        dah = ld16(ar, dao);
     };
 
     float acc[2][16];
@@ -820,16 +833,18 @@ __global__ __launch_bounds__(256, 2) void gemm_q80_kernel(const uint8_t* w, cons
     issue(0);
     for (uint32_t U = 0; U < nst; ++U) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        reinterpret_cast<float*>(lds[U & 1] + k8_da)[tid] = half_bits(dah);  // [block tid / 64][row tid % 64]
+        if (tid < 64 * NB) {
+            reinterpret_cast<float*>(lds[U & 1] + KD)[tid] = half_bits(dah);  // [block tid / 64][row tid % 64]
+        }
         lds_barrier();
         if (U + 1 < nst) {
             issue(U + 1);
         }
         const uint8_t* S = lds[U & 1];
-        const uint8_t* WR = S + (32 * wv + li) * k8_win;
-        const float* da = reinterpret_cast<const float*>(S + k8_da);
+        const uint8_t* WR = S + (32 * wv + li) * WIN;
+        const float* da = reinterpret_cast<const float*>(S + KD);
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < NB; ++b) {
             const uint32_t xd = ow + 34 * b;  // d_w, then 16 bytes for this lane half
             const uint32_t* dwp = reinterpret_cast<const uint32_t*>(WR + (xd & ~3u));
             const float dw = half_bits(__builtin_amdgcn_alignbyte(dwp[1], dwp[0], xd & 3) & 0xFFFF);
@@ -838,7 +853,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q80_kernel(const uint8_t* w, cons
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
                 const uint32_t xa = oa[g] + 34 * b + 2 + 16 * H;
-                const i4v a = lds_bytes16(S + k8_a + (32 * g + li) * k8_win + (xa & ~3u), xa & 3);
+                const i4v a = lds_bytes16(S + KA + (32 * g + li) * WIN + (xa & ~3u), xa & 3);
                 const i16v cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i16v{}, 0, 0, 0);
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
@@ -889,8 +904,8 @@ hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* 
         gemm_q_kernel<qtype_q5_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         break;
     case qtype_q8_0:
-        if (cols % 128 == 0) {
-            gemm_q80_kernel<<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        if (cols % 64 == 0) {  // whole stages
+            gemm_q80_kernel<2><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         } else {
             gemm_q_kernel<qtype_q8_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         }

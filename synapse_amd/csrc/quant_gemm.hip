@@ -709,107 +709,94 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(const uint8_t* w, cons
 // ---- Q8_0 through LDS ------------------------------------------------------------------
 //
 // The Q4_K tile (4 waves, 128 weight rows x 64 activation rows, a wave's 32
-// against all 64) over stages of NB 34-byte blocks (launched with NB = 2: 32
-// KB of LDS, so the whole grid of a 14336-row product is resident at once;
-// NB = 4 measured 4-5 % slower). A row's 34 NB bytes of a stage start at the
-// same byte of a dword in every stage, so each row is copied as a window of
-// whole chunks from the dword at or before it (rows 20 or 36 dwords apart in
-// LDS: distinct banks) and read back realigned by v_alignbyte. The stage's activation scales (64 rows x 4 blocks, one per
+// against all 64) over stages of two 34-byte blocks (64 weights): 32 KB of
+// LDS, so the whole grid of a 14336-row product is resident at once (stages
+// of four blocks measured 4-5 % slower). The interface keeps w and act
+// 4-byte aligned and this kernel runs when cols is a multiple of 64, so
+// every row, and each row's 68 bytes of a stage, start on a dword: a row is
+// copied as the 80-byte window from there (rows 20 dwords apart in LDS), and
+// each block's bytes sit at a shift known at compile time, so the operands
+// are read as two whole 16-byte chunks (conflict-free) and realigned in
+// registers by v_alignbyte (dword reads at a run-time shift measured 205
+// against 152 us: all lanes at the same byte of their chunk hit a quarter of
+// the banks). The stage's activation scales (64 rows x 2 blocks, one per
 // thread) are loaded into registers with the copies and written to LDS as
 // f32 before the stage's barrier. Per block, the reference's
 // float(sumi) (d_w d_a) (S/kernels/dot.hpp, the Q8_0 block kernel).
 
-// NB blocks per stage: a row's 34 NB bytes from any dword start, in a window
-// of 16-byte chunks.
-template <int NB>
-constexpr uint32_t k8_win = NB == 4 ? 144 : 80;
-template <int NB>
-constexpr uint32_t k8_a = 128 * k8_win<NB>;
-template <int NB>
-constexpr uint32_t k8_da = k8_a<NB> + 64 * k8_win<NB>;
-template <int NB>
-constexpr uint32_t k8_stage = k8_da<NB> + NB * 64 * 4;
+constexpr uint32_t k8_win = 80;                      // 5 chunks: a row's 68 bytes of a stage
+constexpr uint32_t k8_a = 128 * k8_win;              // the weight rows' windows, then
+constexpr uint32_t k8_da = k8_a + 64 * k8_win;       // the activation rows', then
+constexpr uint32_t k8_stage = k8_da + 2 * 64 * 4;    // d_a [block][row] as f32
 
-// 16 bytes at byte o (0..3) of the 20 at p (p 4-aligned).
-__device__ __forceinline__ i4v lds_bytes16(const uint8_t* p, uint32_t o) {
-    const uint32_t* d = reinterpret_cast<const uint32_t*>(p);
-    uint32_t w5[5];
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-        w5[k] = d[k];
-    }
-    return i4v{static_cast<int>(__builtin_amdgcn_alignbyte(w5[1], w5[0], o)),
-               static_cast<int>(__builtin_amdgcn_alignbyte(w5[2], w5[1], o)),
-               static_cast<int>(__builtin_amdgcn_alignbyte(w5[3], w5[2], o)),
-               static_cast<int>(__builtin_amdgcn_alignbyte(w5[4], w5[3], o))};
+// 16 bytes at byte M of the two 16-byte chunks at p (p 16-aligned).
+template <uint32_t M>
+__device__ __forceinline__ i4v lds_chunks_at(const uint8_t* p) {
+    const u4 c0 = *reinterpret_cast<const u4*>(p), c1 = *reinterpret_cast<const u4*>(p + 16);
+    const uint32_t w8[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+    constexpr uint32_t k = M / 4, sh = M % 4;
+    return i4v{static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 1], w8[k], sh)),
+               static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 2], w8[k + 1], sh)),
+               static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 3], w8[k + 2], sh)),
+               static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 4], w8[k + 3], sh))};
 }
 
-template <int NB>
-__global__ __launch_bounds__(256, NB == 4 ? 2 : 4) void gemm_q80_kernel(const uint8_t* w, const uint8_t* act,
-                                                                        const float* bias, float* out, uint32_t n,
-                                                                        uint32_t rows, uint32_t cols) {
-    constexpr uint32_t WIN = k8_win<NB>, CH = WIN / 16, SB = 34 * NB;  // chunks per row, bytes per row-stage
-    constexpr uint32_t KA = k8_a<NB>, KD = k8_da<NB>, KS = k8_stage<NB>;
-    constexpr int NW = (32 * CH + 63) / 64, NA = (16 * CH + 63) / 64;  // copies per wave
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][KS];
+__global__ __launch_bounds__(256, 4) void gemm_q80_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
+                                                          float* out, uint32_t n, uint32_t rows, uint32_t cols) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][k8_stage];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t ln = tid & 63, H = ln >> 5, li = ln & 31;
-    const uint32_t nst = cols / (32 * NB);
-    const uint32_t wrow = cols / 32 * 34, arow = wrow;
+    const uint32_t nst = cols / 64;
+    const uint32_t wrow = cols / 32 * 34, arow = wrow;  // multiples of 4
     const uint32_t o0 = blockIdx.x * gq_m + wv * 32;
     const uint32_t t0 = blockIdx.y * gq_n;
 
     // The wave's weight rows and the block's activation rows, each through a
-    // resource from the dword at or before its first byte, rebased per stage;
-    // whole dwords, as a copy's range check is per dword.
+    // resource rebased per stage (rows past the last read zeros).
     const uint32_t wave_rows = o0 < rows ? min(32u, rows - o0) : 0;
-    const uint8_t* wp = w + static_cast<std::size_t>(min(o0, rows - 1)) * wrow;
-    const uint32_t delta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wp) & 3);
-    const uint8_t* wbase = wp - delta;
-    const uint32_t wbytes = (wave_rows * wrow + delta + 3) & ~3u;
-    const uint8_t* ap = act + static_cast<std::size_t>(t0) * arow;
-    const uint32_t adelta = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ap) & 3);
-    const uint8_t* abase = ap - adelta;
-    const uint32_t abytes = (min(gq_n, n - t0) * arow + adelta + 3) & ~3u;
+    const uint8_t* wbase = w + static_cast<std::size_t>(min(o0, rows - 1)) * wrow;
+    const uint32_t wbytes = wave_rows * wrow;
+    const uint8_t* abase = act + static_cast<std::size_t>(t0) * arow;
+    const uint32_t abytes = min(gq_n, n - t0) * arow;
 
-    // Copies: wave wv's 32 weight rows, chunk ch = 64 i + ln of its 288 (row
-    // ch / 9, chunk ch % 9; lanes 0..31 of the fifth copy), and activation
-    // rows 16 wv .. 16 wv + 15, chunk ch of their 144 (lanes 0..15 of the
-    // third). The d_a of row tid % 64, block tid / 64.
-    uint32_t wo[NW], ao[NA];
+    // Copies: wave wv's 32 weight rows, chunk ch = 64 i + ln of their 160
+    // (row ch / 5, chunk ch % 5; lanes 0..31 of the third copy), and
+    // activation rows 16 wv .. 16 wv + 15, chunk ch of their 80 (lanes
+    // 0..15 of the second). The d_a of row tid % 64, block tid / 64
+    // (threads 0..127).
+    uint32_t wo[3], ao[2];
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
+    for (int i = 0; i < 3; ++i) {
         const uint32_t ch = 64 * i + ln;
-        wo[i] = ((delta + ch / CH * wrow) & ~3u) + 16 * (ch % CH);
+        wo[i] = ch / 5 * wrow + 16 * (ch % 5);
     }
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
+    for (int i = 0; i < 2; ++i) {
         const uint32_t ch = 64 * i + ln;
-        ao[i] = ((adelta + (16 * wv + ch / CH) * arow) & ~3u) + 16 * (ch % CH);
+        ao[i] = (16 * wv + ch / 5) * arow + 16 * (ch % 5);
     }
-    const uint32_t dao = adelta + (tid & 63) * arow + (tid >> 6) * 34;
+    const uint32_t dao = (tid & 63) * arow + (tid >> 6) * 34;
 
     const uint32_t L0 = lds_address(&lds[0][0]);
     uint32_t dah = 0;
     const auto issue = [&](uint32_t U) __attribute__((always_inline)) {
-        const uint32_t S = L0 + (U & 1) * KS;
-        const rsrc wr = make_rsrc(wbase + U * SB, wave_rows != 0 ? wbytes - U * SB : 0);
-        const rsrc ar = make_rsrc(abase + U * SB, abytes - U * SB);
+        const uint32_t S = L0 + (U & 1) * k8_stage;
+        const rsrc wr = make_rsrc(wbase + U * 68, wave_rows != 0 ? wbytes - U * 68 : 0);
+        const rsrc ar = make_rsrc(abase + U * 68, abytes - U * 68);
 #pragma unroll
-        for (int i = 0; i < NW; ++i) {
-            if (64 * i + 64 <= 32 * CH || ln < 32 * CH - 64 * i) {
-                copy16_lds(wr, S + 32 * WIN * wv + 1024 * i, wo[i]);
-            }
+        for (int i = 0; i < 2; ++i) {
+            copy16_lds(wr, S + 32 * k8_win * wv + 1024 * i, wo[i]);
         }
-#pragma unroll
-        for (int i = 0; i < NA; ++i) {
-            if (64 * i + 64 <= 16 * CH || ln < 16 * CH - 64 * i) {
-                copy16_lds(ar, S + KA + 16 * WIN * wv + 1024 * i, ao[i]);
-            }
+        copy16_lds(ar, S + k8_a + 16 * k8_win * wv, ao[0]);
+        if (ln < 32) {
+            copy16_lds(wr, S + 32 * k8_win * wv + 2048, wo[2]);
         }
-        if (tid < 64 * NB) {
+        if (ln < 16) {
+            copy16_lds(ar, S + k8_a + 16 * k8_win * wv + 1024, ao[1]);
+        }
+        if (tid < 128) {
             dah = ld16(ar, dao);
         }
     };
@@ -822,38 +809,29 @@ __global__ __launch_bounds__(256, NB == 4 ? 2 : 4) void gemm_q80_kernel(const ui
             acc[g][i] = 0.0f;
         }
     }
-    // Byte of a dword where this lane's weight row and activation rows start.
-    const uint32_t ow = (delta + li * wrow) & 3;
-    uint32_t oa[2];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        oa[g] = (adelta + (32 * g + li) * arow) & 3;
-    }
 
     issue(0);
     for (uint32_t U = 0; U < nst; ++U) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (tid < 64 * NB) {
-            reinterpret_cast<float*>(lds[U & 1] + KD)[tid] = half_bits(dah);  // [block tid / 64][row tid % 64]
+        if (tid < 128) {
+            reinterpret_cast<float*>(lds[U & 1] + k8_da)[tid] = half_bits(dah);
         }
         lds_barrier();
         if (U + 1 < nst) {
             issue(U + 1);
         }
         const uint8_t* S = lds[U & 1];
-        const uint8_t* WR = S + (32 * wv + li) * WIN;
-        const float* da = reinterpret_cast<const float*>(S + KD);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const uint32_t xd = ow + 34 * b;  // d_w, then 16 bytes for this lane half
-            const uint32_t* dwp = reinterpret_cast<const uint32_t*>(WR + (xd & ~3u));
-            const float dw = half_bits(__builtin_amdgcn_alignbyte(dwp[1], dwp[0], xd & 3) & 0xFFFF);
-            const uint32_t xq = xd + 2 + 16 * H;
-            const i4v q = lds_bytes16(WR + (xq & ~3u), xq & 3);
+        const uint8_t* WR = S + (32 * wv + li) * k8_win;
+        const float* da = reinterpret_cast<const float*>(S + k8_da);
+        const auto block = [&]<int b>() __attribute__((always_inline)) {
+            // d_w at byte 34 b of the row; this lane half's 16 bytes at
+            // 34 b + 2 + 16 H: chunks C + 16 H and the next, from byte M.
+            constexpr uint32_t C = (34 * b + 2) / 16 * 16, M = (34 * b + 2) % 16;
+            const float dw = half_bits(*reinterpret_cast<const uint16_t*>(WR + 34 * b));
+            const i4v q = lds_chunks_at<M>(WR + C + 16 * H);
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
-                const uint32_t xa = oa[g] + 34 * b + 2 + 16 * H;
-                const i4v a = lds_bytes16(S + KA + (32 * g + li) * WIN + (xa & ~3u), xa & 3);
+                const i4v a = lds_chunks_at<M>(S + k8_a + (32 * g + li) * k8_win + C + 16 * H);
                 const i16v cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i16v{}, 0, 0, 0);
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
@@ -864,7 +842,9 @@ __global__ __launch_bounds__(256, NB == 4 ? 2 : 4) void gemm_q80_kernel(const ui
                     }
                 }
             }
-        }
+        };
+        block.template operator()<0>();
+        block.template operator()<1>();
     }
 
     const uint32_t o = o0 + li;
@@ -882,7 +862,6 @@ __global__ __launch_bounds__(256, NB == 4 ? 2 : 4) void gemm_q80_kernel(const ui
         }
     }
 }
-
 }  // namespace
 
 hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* act, const float* bias, float* out,
@@ -904,8 +883,8 @@ hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* 
         gemm_q_kernel<qtype_q5_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         break;
     case qtype_q8_0:
-        if (cols % 64 == 0) {  // whole stages
-            gemm_q80_kernel<2><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        if (cols % 64 == 0 && (reinterpret_cast<uintptr_t>(w) & 3) == 0 && (reinterpret_cast<uintptr_t>(act) & 3) == 0) {
+            gemm_q80_kernel<<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         } else {
             gemm_q_kernel<qtype_q8_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         }

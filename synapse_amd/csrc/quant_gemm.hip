@@ -15,20 +15,20 @@
 //
 // so each block's integers are ggml's and results differ from its gemv only
 // by float association. Three kernels:
-// - gemm_q_kernel (Q4_0, Q5_0, Q8_0): a workgroup (4 waves) owns 128 weight
-//   rows x 64 activation rows; a wave 32 weight rows (one per lane, the
-//   product's B operand) against the 64 activation rows (two A operands).
-//   Every lane loads its own weight row's bytes and its activation rows'
-//   bytes into registers, two batches of steps in flight; the weights are
-//   decoded to signed int8 in registers. The activation scales of the
-//   block's 64 rows are staged in LDS for 128 steps of 32 at a time.
-// - gemm_q4k_kernel (Q4_K): the same tile; each 256-block's weight and
-//   activation bytes reach LDS through whole-line direct copies, two stages
-//   deep; the sub-block scales are folded into two int8 weight planes and the
-//   mins take one f16 product per block.
+// - gemm_q4k_kernel (Q4_K): a workgroup (4 waves) owns 128 weight rows x 64
+//   activation rows; a wave 32 weight rows (one per lane, the product's B
+//   operand) against the 64 activation rows (two A operands). Each
+//   256-block's weight and activation bytes reach LDS through whole-line
+//   direct copies, two stages deep; the sub-block scales are folded into two
+//   int8 weight planes and the mins take one f16 product per block.
 // - gemm_q6k_kernel (Q6_K): 64 x 64 per workgroup, 32 x 32 per wave, the
 //   same LDS staging; unsigned quants, the offset through the activation
 //   sums on one f16 product per block.
+// - gemm_qb32_kernel (Q4_0, Q5_0, Q8_0): the Q4_K tile, stages of two
+//   32-blocks read at compile-time shifts.
+// - gemm_q_kernel (the same three when cols is not a multiple of 64): the
+//   same tile, every lane loading its own weight row's and activation rows'
+//   bytes into registers, two batches of steps in flight.
 // Details at each kernel.
 
 #include "quant.hpp"
@@ -706,50 +706,63 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(const uint8_t* w, cons
 }
 
 
-// ---- Q8_0 through LDS ------------------------------------------------------------------
+// ---- Q4_0, Q5_0, Q8_0 through LDS ------------------------------------------------------
 //
 // The Q4_K tile (4 waves, 128 weight rows x 64 activation rows, a wave's 32
-// against all 64) over stages of two 34-byte blocks (64 weights): 32 KB of
+// against all 64) over stages of two 32-blocks (64 weights): 20-32 KB of
 // LDS, so the whole grid of a 14336-row product is resident at once (stages
-// of four blocks measured 4-5 % slower). The interface keeps w and act
+// of four Q8_0 blocks measured 4-5 % slower). The interface keeps w and act
 // 4-byte aligned and this kernel runs when cols is a multiple of 64, so
-// every row, and each row's 68 bytes of a stage, start on a dword: a row is
-// copied as the 80-byte window from there (rows 20 dwords apart in LDS), and
-// each block's bytes sit at a shift known at compile time, so the operands
-// are read as two whole 16-byte chunks (conflict-free) and realigned in
-// registers by v_alignbyte (dword reads at a run-time shift measured 205
-// against 152 us: all lanes at the same byte of their chunk hit a quarter of
-// the banks). The stage's activation scales (64 rows x 2 blocks, one per
-// thread) are loaded into registers with the copies and written to LDS as
-// f32 before the stage's barrier. Per block, the reference's
-// float(sumi) (d_w d_a) (S/kernels/dot.hpp, the Q8_0 block kernel).
+// every row, and each row's two blocks of a stage (36, 44 or 68 bytes;
+// activations always Q8_0's 68), start on a dword: a row is copied as the
+// window of whole 16-byte chunks from there (48 or 80 bytes: rows 12 or 20
+// dwords apart in LDS, distinct banks), and each block's bytes sit at a
+// shift known at compile time, so the operands are read as two whole chunks
+// (conflict-free) and realigned in registers by v_alignbyte (Q8_0 read in
+// dwords at a run-time shift measured 205 against 152 us: all lanes at the
+// same byte of their chunk hit a quarter of the banks). The stage's
+// activation scales (64 rows x 2 blocks, one per thread) are loaded into
+// registers with the copies and written to LDS as f32 before the stage's
+// barrier. Per block, the reference's block kernels (S/kernels/dot.hpp:
+// 102-163): sum (q - z) a with z = 8, 16, 0, as float(sumi) (d_w d_a); the
+// weights are decoded to their signed values.
 
-constexpr uint32_t k8_win = 80;                      // 5 chunks: a row's 68 bytes of a stage
-constexpr uint32_t k8_a = 128 * k8_win;              // the weight rows' windows, then
-constexpr uint32_t k8_da = k8_a + 64 * k8_win;       // the activation rows', then
-constexpr uint32_t k8_stage = k8_da + 2 * 64 * 4;    // d_a [block][row] as f32
+template <uint32_t T>
+constexpr uint32_t k32_wwin = T == qtype_q8_0 ? 80 : 48;  // a weight row's window over 2 blocks
+constexpr uint32_t k32_awin = 80;                          // an activation row's (Q8_0 blocks)
+template <uint32_t T>
+constexpr uint32_t k32_a = 128 * k32_wwin<T>;
+template <uint32_t T>
+constexpr uint32_t k32_da = k32_a<T> + 64 * k32_awin;
+template <uint32_t T>
+constexpr uint32_t k32_stage = k32_da<T> + 2 * 64 * 4;  // d_a [block][row] as f32
 
-// 16 bytes at byte M of the two 16-byte chunks at p (p 16-aligned).
-template <uint32_t M>
-__device__ __forceinline__ i4v lds_chunks_at(const uint8_t* p) {
+// N dwords from byte M of the two 16-byte chunks at p (p 16-aligned).
+template <uint32_t M, int N>
+__device__ __forceinline__ void lds_chunk_words(const uint8_t* p, uint32_t (&d)[N]) {
     const u4 c0 = *reinterpret_cast<const u4*>(p), c1 = *reinterpret_cast<const u4*>(p + 16);
     const uint32_t w8[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
     constexpr uint32_t k = M / 4, sh = M % 4;
-    return i4v{static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 1], w8[k], sh)),
-               static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 2], w8[k + 1], sh)),
-               static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 3], w8[k + 2], sh)),
-               static_cast<int>(__builtin_amdgcn_alignbyte(w8[k + 4], w8[k + 3], sh))};
+    static_assert(k + N < 8 || (k + N == 8 && sh == 0), "past the two chunks");
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        d[j] = __builtin_amdgcn_alignbyte(w8[(k + j + 1) & 7], w8[k + j], sh);
+    }
 }
 
-__global__ __launch_bounds__(256, 4) void gemm_q80_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
-                                                          float* out, uint32_t n, uint32_t rows, uint32_t cols) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][k8_stage];
+template <uint32_t T>
+__global__ __launch_bounds__(256, 4) void gemm_qb32_kernel(const uint8_t* w, const uint8_t* act, const float* bias,
+                                                           float* out, uint32_t n, uint32_t rows, uint32_t cols) {
+    constexpr uint32_t BB = block_bytes<T>, WWIN = k32_wwin<T>, WCH = WWIN / 16;
+    constexpr uint32_t KA = k32_a<T>, KD = k32_da<T>, KS = k32_stage<T>;
+    constexpr int NW = (32 * WCH + 63) / 64, NA = (16 * 5 + 63) / 64;  // copies per wave
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][KS];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t ln = tid & 63, H = ln >> 5, li = ln & 31;
     const uint32_t nst = cols / 64;
-    const uint32_t wrow = cols / 32 * 34, arow = wrow;  // multiples of 4
+    const uint32_t wrow = cols / 32 * BB, arow = cols / 32 * 34;  // multiples of 4
     const uint32_t o0 = blockIdx.x * gq_m + wv * 32;
     const uint32_t t0 = blockIdx.y * gq_n;
 
@@ -761,19 +774,19 @@ __global__ __launch_bounds__(256, 4) void gemm_q80_kernel(const uint8_t* w, cons
     const uint8_t* abase = act + static_cast<std::size_t>(t0) * arow;
     const uint32_t abytes = min(gq_n, n - t0) * arow;
 
-    // Copies: wave wv's 32 weight rows, chunk ch = 64 i + ln of their 160
-    // (row ch / 5, chunk ch % 5; lanes 0..31 of the third copy), and
-    // activation rows 16 wv .. 16 wv + 15, chunk ch of their 80 (lanes
-    // 0..15 of the second). The d_a of row tid % 64, block tid / 64
-    // (threads 0..127).
-    uint32_t wo[3], ao[2];
+    // Copies: wave wv's 32 weight rows, chunk ch = 64 i + ln of their 32 WCH
+    // (row ch / WCH, chunk ch % WCH), and activation rows 16 wv .. 16 wv +
+    // 15, chunk ch of their 80 (row ch / 5); the last copy of each with the
+    // lanes that remain. The d_a of row tid % 64, block tid / 64 (threads
+    // 0..127).
+    uint32_t wo[NW], ao[NA];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < NW; ++i) {
         const uint32_t ch = 64 * i + ln;
-        wo[i] = ch / 5 * wrow + 16 * (ch % 5);
+        wo[i] = ch / WCH * wrow + 16 * (ch % WCH);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NA; ++i) {
         const uint32_t ch = 64 * i + ln;
         ao[i] = (16 * wv + ch / 5) * arow + 16 * (ch % 5);
     }
@@ -782,19 +795,20 @@ __global__ __launch_bounds__(256, 4) void gemm_q80_kernel(const uint8_t* w, cons
     const uint32_t L0 = lds_address(&lds[0][0]);
     uint32_t dah = 0;
     const auto issue = [&](uint32_t U) __attribute__((always_inline)) {
-        const uint32_t S = L0 + (U & 1) * k8_stage;
-        const rsrc wr = make_rsrc(wbase + U * 68, wave_rows != 0 ? wbytes - U * 68 : 0);
+        const uint32_t S = L0 + (U & 1) * KS;
+        const rsrc wr = make_rsrc(wbase + U * 2 * BB, wave_rows != 0 ? wbytes - U * 2 * BB : 0);
         const rsrc ar = make_rsrc(abase + U * 68, abytes - U * 68);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            copy16_lds(wr, S + 32 * k8_win * wv + 1024 * i, wo[i]);
+        for (int i = 0; i < NW; ++i) {
+            if (64 * i + 64 <= 32 * WCH || ln < 32 * WCH - 64 * i) {
+                copy16_lds(wr, S + 32 * WWIN * wv + 1024 * i, wo[i]);
+            }
         }
-        copy16_lds(ar, S + k8_a + 16 * k8_win * wv, ao[0]);
-        if (ln < 32) {
-            copy16_lds(wr, S + 32 * k8_win * wv + 2048, wo[2]);
-        }
-        if (ln < 16) {
-            copy16_lds(ar, S + k8_a + 16 * k8_win * wv + 1024, ao[1]);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            if (64 * i + 64 <= 80 || ln < 80 - 64 * i) {
+                copy16_lds(ar, S + KA + 16 * k32_awin * wv + 1024 * i, ao[i]);
+            }
         }
         if (tid < 128) {
             dah = ld16(ar, dao);
@@ -814,25 +828,49 @@ __global__ __launch_bounds__(256, 4) void gemm_q80_kernel(const uint8_t* w, cons
     for (uint32_t U = 0; U < nst; ++U) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (tid < 128) {
-            reinterpret_cast<float*>(lds[U & 1] + k8_da)[tid] = half_bits(dah);
+            reinterpret_cast<float*>(lds[U & 1] + KD)[tid] = half_bits(dah);
         }
         lds_barrier();
         if (U + 1 < nst) {
             issue(U + 1);
         }
         const uint8_t* S = lds[U & 1];
-        const uint8_t* WR = S + (32 * wv + li) * k8_win;
-        const float* da = reinterpret_cast<const float*>(S + k8_da);
+        const uint8_t* WR = S + (32 * wv + li) * WWIN;
+        const float* da = reinterpret_cast<const float*>(S + KD);
         const auto block = [&]<int b>() __attribute__((always_inline)) {
-            // d_w at byte 34 b of the row; this lane half's 16 bytes at
-            // 34 b + 2 + 16 H: chunks C + 16 H and the next, from byte M.
-            constexpr uint32_t C = (34 * b + 2) / 16 * 16, M = (34 * b + 2) % 16;
-            const float dw = half_bits(*reinterpret_cast<const uint16_t*>(WR + 34 * b));
-            const i4v q = lds_chunks_at<M>(WR + C + 16 * H);
+            // d_w at byte BB b of the row, then the block's quants.
+            const float dw = half_bits(*reinterpret_cast<const uint16_t*>(WR + BB * b));
+            uint32_t q[4];
+            if constexpr (T == qtype_q8_0) {  // this lane half's 16 bytes at 34 b + 2 + 16 H
+                constexpr uint32_t C = (34 * b + 2) / 16 * 16, M = (34 * b + 2) % 16;
+                lds_chunk_words<M>(WR + C + 16 * H, q);
+            } else if constexpr (T == qtype_q4_0) {  // 16 bytes at 18 b + 2, this lane half's nibbles
+                constexpr uint32_t C = (18 * b + 2) / 16 * 16, M = (18 * b + 2) % 16;
+                uint32_t qs[4];
+                lds_chunk_words<M>(WR + C, qs);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    q[j] = sext4((qs[j] >> (4 * H)) & 0x0F0F0F0Fu);
+                }
+            } else {  // Q5_0: the 32 high bits at 22 b + 2, then 16 bytes
+                constexpr uint32_t C = (22 * b + 2) / 16 * 16, M = (22 * b + 2) % 16;
+                uint32_t hq[5];
+                lds_chunk_words<M>(WR + C, hq);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    q[j] = sext5(((hq[1 + j] >> (4 * H)) & 0x0F0F0F0Fu) | spread4((hq[0] >> (16 * H + 4 * j)) & 0xF));
+                }
+            }
+            const i4v qv = {static_cast<int>(q[0]), static_cast<int>(q[1]), static_cast<int>(q[2]),
+                            static_cast<int>(q[3])};
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
-                const i4v a = lds_chunks_at<M>(S + k8_a + (32 * g + li) * k8_win + C + 16 * H);
-                const i16v cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q, i16v{}, 0, 0, 0);
+                constexpr uint32_t CA = (34 * b + 2) / 16 * 16, MA = (34 * b + 2) % 16;
+                uint32_t av[4];
+                lds_chunk_words<MA>(S + KA + (32 * g + li) * k32_awin + CA + 16 * H, av);
+                const i4v a = {static_cast<int>(av[0]), static_cast<int>(av[1]), static_cast<int>(av[2]),
+                               static_cast<int>(av[3])};
+                const i16v cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qv, i16v{}, 0, 0, 0);
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
                     const f4 d4 = *reinterpret_cast<const f4*>(da + 64 * b + 32 * g + 8 * qd + 4 * H);
@@ -875,16 +913,29 @@ hipError_t launch_gemm_q(uint32_t t, const uint8_t* w, const float* x, uint8_t* 
         quantize_act_kernel<false><<<qblocks, 256, 0, stream>>>(x, act, n, cols);
     }
     const dim3 grid((rows + gq_m - 1) / gq_m, (n + gq_n - 1) / gq_n);
+    // The 32-block formats through LDS when every row's stage starts on a
+    // dword (whole stages of two blocks; w and act 4-byte aligned, as the
+    // interface keeps them); else the register kernel.
+    const bool staged = cols % 64 == 0 && (reinterpret_cast<uintptr_t>(w) & 3) == 0 &&
+                        (reinterpret_cast<uintptr_t>(act) & 3) == 0;
     switch (t) {
     case qtype_q4_0:
-        gemm_q_kernel<qtype_q4_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        if (staged) {
+            gemm_qb32_kernel<qtype_q4_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        } else {
+            gemm_q_kernel<qtype_q4_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        }
         break;
     case qtype_q5_0:
-        gemm_q_kernel<qtype_q5_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        if (staged) {
+            gemm_qb32_kernel<qtype_q5_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        } else {
+            gemm_q_kernel<qtype_q5_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        }
         break;
     case qtype_q8_0:
-        if (cols % 64 == 0 && (reinterpret_cast<uintptr_t>(w) & 3) == 0 && (reinterpret_cast<uintptr_t>(act) & 3) == 0) {
-            gemm_q80_kernel<<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
+        if (staged) {
+            gemm_qb32_kernel<qtype_q8_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         } else {
             gemm_q_kernel<qtype_q8_0><<<grid, 256, 0, stream>>>(w, act, bias, out, n, rows, cols);
         }

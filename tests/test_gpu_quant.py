@@ -105,12 +105,14 @@ def test_matmul_q_matches_host_blocks(arena, t, n, rows, cols):
 
 @pytest.mark.parametrize("t", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])
 @pytest.mark.parametrize("n,rows,cols", [(32, 37, 512), (70, 130, 2048), (64, 128, 4096), (33, 300, 256),
-                                         (129, 33, 768)])
+                                         (129, 33, 768), (40, 50, 800)])
 def test_matmul_q_gemm_matches_host(arena, t, n, rows, cols):
     """From 32 activation rows on, the product runs on the int8 matrix cores;
     the activation bytes stay ggml's bit for bit and every output is within
     1e-5 of sum |w| |x^| of the exact product of the dequantized operands
-    (each block's integer sum is exact; only float association differs)."""
+    (each block's integer sum is exact; only float association differs).
+    800 columns (25 blocks, not whole two-block stages) take the 32-block
+    formats' register kernel, the others their LDS kernels."""
     if cols % BLOCK[t][0]:
         pytest.skip("cols not whole blocks")
     rng = np.random.default_rng(7000 + 31 * t + n)

@@ -131,6 +131,31 @@ def test_matmul_q_gemm_matches_host(arena, t, n, rows, cols):
     assert np.all(err <= 1e-5 * np.maximum(scale, 1.0)), float((err / np.maximum(scale, 1.0)).max())
 
 
+@pytest.mark.parametrize("t,rows,cols", [(Q4_K, 2048, 4096), (Q6_K, 1024, 14336), (Q8_0, 2048, 4096),
+                                         (Q4_0, 2048, 4096), (Q5_0, 2048, 4096)])
+def test_gemm_at_model_size_matches_the_gemv(arena, t, rows, cols):
+    """Llama-3-8B row lengths (ffn_up's 4096 columns, ffn_down's 14336),
+    128 activation rows: many workgroups in both dimensions and every stage
+    of a long row (the row counts are cut to keep the host's bound quick). The GEMM (int8 matrix cores,
+    LDS-staged) and the GEMV (v_dot4, one wave per row) are separate kernels
+    over the same exact block integers, so they agree within twice the
+    float-association bound, 2e-5 of sum |w| |x^|; the activation bytes are
+    ggml's bit for bit."""
+    rng = np.random.default_rng(9000 + t)
+    raw = random_blocks(t, rows, cols, rng)
+    n = 128
+    x = rng.standard_normal((n, cols)).astype(np.float32)
+    gemm, act = matmul_q(arena, raw, t, x, rows, cols)
+    gemv = np.concatenate([matmul_q(arena, raw, t, x[i:i + 16], rows, cols)[0] for i in range(0, n, 16)])
+    want_act = np.concatenate([qh.quantize_act(x[r], t) for r in range(n)])
+    assert np.array_equal(act, want_act)
+    w_abs = np.abs(qh.dequantize(raw, t).reshape(rows, cols))
+    xa = np.abs(np.stack([qh.dequantize_act(a, qh.act_type(t)) for a in want_act.reshape(n, -1)]))
+    scale = (xa @ w_abs.T).astype(np.float64)
+    err = np.abs(gemm.astype(np.float64) - gemv.astype(np.float64))
+    assert np.all(err <= 2e-5 * np.maximum(scale, 1.0)), float((err / np.maximum(scale, 1.0)).max())
+
+
 @pytest.mark.parametrize("t", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])
 def test_embed_quantized_table_bit_exact(arena, t):
     rng = np.random.default_rng(7 + t)

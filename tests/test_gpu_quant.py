@@ -105,7 +105,7 @@ def test_matmul_q_matches_host_blocks(arena, t, n, rows, cols):
 
 @pytest.mark.parametrize("t", [Q4_0, Q5_0, Q8_0, Q4_K, Q6_K])
 @pytest.mark.parametrize("n,rows,cols", [(32, 37, 512), (70, 130, 2048), (64, 128, 4096), (33, 300, 256),
-                                         (129, 33, 768), (40, 50, 800)])
+                                         (129, 33, 768), (40, 50, 800), (32, 1, 256), (65, 3, 512), (32, 2, 64)])
 def test_matmul_q_gemm_matches_host(arena, t, n, rows, cols):
     """From 32 activation rows on, the product runs on the int8 matrix cores;
     the activation bytes stay ggml's bit for bit and every output is within
